@@ -1,0 +1,317 @@
+#!/usr/bin/env python3
+"""Benchmark of the TensorPlay PrivateUse1 hot path on one MI355X.
+
+Headline workload ("broadcast elementwise"): one
+step runs the config-2 operator set on a [8192, 8192] tensor in float32 and
+in bfloat16 storage -- add/sub/mul/div against a row-broadcast [8192] and a
+column-broadcast [8192, 1] operand, their in-place forms, the scalar forms,
+exp, log(|a|+1e-3), sqrt(|a|), pow(a, 2), relu, gelu, sigmoid, and the relu /
+gelu / sigmoid backward kernels -- through the library's operator C-ABI, with
+every input already resident in HBM.  ``value`` is the algorithmic bytes of
+one step (2 N^2 e per forward op, 3 N^2 e per backward op; the broadcast
+operand is not counted) times the steps, divided by the wall time of the
+timed steps.
+
+Also reported on the same line:
+* ``roofline``: the dominant kernel (the broadcasting binary kernel, float32
+  add against a row-broadcast operand), its average launch duration from
+  HIP events recorded on the library's own stream, against 8 TB/s;
+* ``suite``: per-kernel throughput of configs 2-5 (GB/s or TFLOP/s and the
+  fraction of the matching MI355X peak), each from HIP events;
+* ``cpu_baseline``: the repository's C oracle (a CPU port of the same
+  operators, float64 arithmetic, OpenMP) timed on this host on a bounded
+  sample of the same workload.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
+METRIC = "GEMM TFLOP/s + %MFMA peak; reduce/softmax/eltwise GB/s + %HBM peak"
+N = 8192
+
+amd = importlib.import_module("tensorplay-mlu_amd")
+F32, F16, BF16 = 0, 1, 2
+ESIZE = {F32: 4, BF16: 2, F16: 2}
+NAME = {F32: "fp32", BF16: "bf16", F16: "fp16"}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Events:
+    """A pair of HIP events on the library's stream."""
+
+    def __init__(self, lib):
+        import ctypes as C
+        self.C, self.lib = C, lib
+        self.start, self.stop = C.c_void_p(), C.c_void_p()
+        assert lib.tp_amd_event_create(C.byref(self.start)) == 0
+        assert lib.tp_amd_event_create(C.byref(self.stop)) == 0
+
+    def time_ms(self, fn, reps: int) -> float:
+        """Average milliseconds of ``fn`` over ``reps`` back-to-back calls."""
+        C, lib = self.C, self.lib
+        assert lib.tp_amd_event_record(self.start, 0) == 0
+        for _ in range(reps):
+            fn()
+        assert lib.tp_amd_event_record(self.stop, 0) == 0
+        ms = C.c_float()
+        assert lib.tp_amd_event_elapsed_ms(self.start, self.stop, C.byref(ms)) == 0
+        return ms.value / reps
+
+
+def build_config2(ops, dev, dtype):
+    """Resident inputs of config 2 in ``dtype`` (generated in float32 on the
+    host, converted on the device)."""
+    g = np.random.default_rng(0)
+    a32 = g.standard_normal((N, N), dtype=np.float32)
+    row32 = g.uniform(0.5, 2.0, N).astype(np.float32)
+    col32 = g.uniform(0.5, 2.0, (N, 1)).astype(np.float32)
+    g32 = g.standard_normal((N, N), dtype=np.float32)
+
+    def put(x):
+        d = dev.from_numpy(x)
+        return d if dtype == F32 else ops.to(d, dtype)
+
+    a, row, col, grad = put(a32), put(row32), put(col32), put(g32)
+    absa = ops.abs(a)
+    loga = ops.add_scalar(absa, 1e-3)
+    work = ops.clone(a)
+    y = ops.sigmoid(a)
+    return dict(a=a, row=row, col=col, grad=grad, absa=absa, loga=loga, work=work, y=y)
+
+
+def config2_ops(ops, t):
+    """(name, callable, bytes-per-element factor) for one pass of config 2."""
+    a, row, col, grad, work = t["a"], t["row"], t["col"], t["grad"], t["work"]
+    fwd, bwd = 2, 3
+    return [
+        ("add_row", lambda: ops.add(a, row), fwd), ("sub_row", lambda: ops.sub(a, row), fwd),
+        ("mul_row", lambda: ops.mul(a, row), fwd), ("div_row", lambda: ops.div(a, row), fwd),
+        ("add_col", lambda: ops.add(a, col), fwd), ("sub_col", lambda: ops.sub(a, col), fwd),
+        ("mul_col", lambda: ops.mul(a, col), fwd), ("div_col", lambda: ops.div(a, col), fwd),
+        ("add_", lambda: ops.add_(work, row), fwd), ("sub_", lambda: ops.sub_(work, row), fwd),
+        ("mul_", lambda: ops.mul_(work, row), fwd), ("div_", lambda: ops.div_(work, row), fwd),
+        ("add_scalar", lambda: ops.add_scalar(a, 2.0), fwd),
+        ("sub_scalar", lambda: ops.sub_scalar(a, 2.0), fwd),
+        ("mul_scalar", lambda: ops.mul_scalar(a, 3.0), fwd),
+        ("div_scalar", lambda: ops.div_scalar(a, 4.0), fwd),
+        ("exp", lambda: ops.exp(a), fwd), ("log", lambda: ops.log(t["loga"]), fwd),
+        ("sqrt", lambda: ops.sqrt(t["absa"]), fwd), ("pow2", lambda: ops.pow_scalar(a, 2), fwd),
+        ("relu", lambda: ops.relu(a), fwd), ("gelu", lambda: ops.gelu(a), fwd),
+        ("sigmoid", lambda: ops.sigmoid(a), fwd),
+        ("relu_backward", lambda: ops.threshold_backward(grad, a, 0), bwd),
+        ("gelu_backward", lambda: ops.gelu_backward(grad, a), bwd),
+        ("sigmoid_backward", lambda: ops.sigmoid_backward(grad, t["y"]), bwd),
+    ]
+
+
+def dominant_kernel(lib, ev, t, reps=50):
+    """Average launch duration of the broadcasting binary kernel (fp32 add
+    with a row-broadcast operand), called through the kernel-level C-ABI."""
+    import ctypes as C
+    a, row, out = t["a"], t["row"], t["out"]
+    sizes = (C.c_int64 * 2)(N, N)
+    sa = (C.c_int64 * 2)(N, 1)
+    sb = (C.c_int64 * 2)(0, 1)
+
+    def launch():
+        st = lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, a.data_ptr, sa, row.data_ptr, sb,
+                                      out.data_ptr, sa, 1.0)
+        assert st == 0
+
+    for _ in range(5):
+        launch()
+    ms = ev.time_ms(launch, reps)
+    algo = 2 * N * N * 4
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {"kernel": "binary2d_kernel<float, full, row-broadcast> (add)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "avg_us": round(ms * 1e3, 2), "algorithmic_bytes_per_launch": algo}
+
+
+def suite_config2(ops, ev, tensors):
+    out = {}
+    for dtype, t in tensors.items():
+        for name, fn, factor in config2_ops(ops, t):
+            for _ in range(2):
+                fn()
+            ms = ev.time_ms(fn, 10)
+            gbs = factor * N * N * ESIZE[dtype] / (ms * 1e-3) / 1e9
+            out[f"{name}_{NAME[dtype]}"] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1),
+                                            "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)}
+    return out
+
+
+def suite_config3(ops, dev, ev):
+    out = {}
+    for shape, std in (((32768, 4096), 2.0), ((4096, 32000), 4.0)):
+        x32 = np.random.default_rng(0).standard_normal(shape, dtype=np.float32) * np.float32(std)
+        g32 = np.random.default_rng(1).standard_normal(shape, dtype=np.float32)
+        for dtype in (F32, BF16):
+            x, g = dev.from_numpy(x32), dev.from_numpy(g32)
+            if dtype != F32:
+                x, g = ops.to(x, dtype), ops.to(g, dtype)
+            y = ops.softmax(x, -1)
+            ly = ops.log_softmax(x, -1)
+            n = shape[0] * shape[1] * ESIZE[dtype]
+            tag = f"{shape[0]}x{shape[1]}_{NAME[dtype]}"
+            cases = []
+            for dim in (-1, 0):
+                outb = (shape[0] if dim == -1 else shape[1]) * ESIZE[dtype]
+                cases += [(f"sum_dim{dim}", lambda dim=dim: ops.sum_dim(x, dim), n + outb),
+                          (f"mean_dim{dim}", lambda dim=dim: ops.mean_dim(x, dim), n + outb),
+                          (f"amax_dim{dim}", lambda dim=dim: ops.amax(x, dim), n + outb),
+                          (f"amin_dim{dim}", lambda dim=dim: ops.amin(x, dim), n + outb)]
+            cases += [("softmax", lambda: ops.softmax(x, -1), 2 * n),
+                      ("log_softmax", lambda: ops.log_softmax(x, -1), 2 * n),
+                      ("softmax_backward", lambda: ops._softmax_backward_data(g, y, -1, dtype), 3 * n),
+                      ("log_softmax_backward",
+                       lambda: ops._log_softmax_backward_data(g, ly, -1, dtype), 3 * n)]
+            for name, fn, nbytes in cases:
+                for _ in range(2):
+                    fn()
+                ms = ev.time_ms(fn, 10)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                out[f"{name}_{tag}"] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1),
+                                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)}
+            del x, g, y, ly
+    return out
+
+
+def cpu_baseline(rows: int = 1024):
+    """The C oracle (CPU port, float64 arithmetic, OpenMP) on the first
+    ``rows`` rows of config 2, both dtypes; GB/s of algorithmic bytes."""
+    from oracle import binding as orc
+
+    g = np.random.default_rng(0)
+    a = g.standard_normal((rows, N), dtype=np.float32)
+    row = g.uniform(0.5, 2.0, N).astype(np.float32)
+    col = g.uniform(0.5, 2.0, (rows, 1)).astype(np.float32)
+    grad = g.standard_normal((rows, N), dtype=np.float32)
+    total_bytes, t0 = 0, time.perf_counter()
+    for dtype in (F32, BF16):
+        A, R, Cc, G = (orc.from_float(v, dtype) for v in (a, row, col, grad))
+        absa = orc.unary(5, dtype, A)
+        loga = orc.affine(dtype, absa, 1.0, 1e-3)
+        e = ESIZE[dtype] * rows * N
+        for b in (R, Cc):
+            for op, alpha in ((0, 1.0), (0, -1.0), (1, 1.0), (2, 1.0)):
+                orc.binary(op, dtype, A, b, alpha)
+                total_bytes += 2 * e
+        work = A.copy()
+        for op, alpha in ((0, 1.0), (0, -1.0), (1, 1.0), (2, 1.0)):
+            orc.binary(op, dtype, work, R, alpha, out=work)
+            total_bytes += 2 * e
+        for al, be in ((1.0, 2.0), (1.0, -2.0), (3.0, 0.0), (0.25, 0.0)):
+            orc.affine(dtype, A, al, be)
+            total_bytes += 2 * e
+        for op, x in ((0, A), (1, loga), (2, absa), (6, A), (8, A), (12, A), (9, A)):
+            orc.unary(op, dtype, x)
+            total_bytes += 2 * e
+        y = orc.unary(9, dtype, A)
+        for op, s in ((0, A), (3, A), (1, y)):
+            orc.activation_backward(op, dtype, G, s)
+            total_bytes += 3 * e
+    secs = time.perf_counter() - t0
+    return {"value": round(total_bytes / secs / 1e9, 3), "unit": "GB/s",
+            "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+            "seconds": round(secs, 2),
+            "sample": f"config-2 operator set on the first {rows} of {N} rows, fp32 and bf16 "
+                      "(repository C oracle, float64 arithmetic; TensorPlay's CPU path is not "
+                      "installed)"}
+
+
+def main() -> int:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-suite", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        return 2
+
+    lib = amd.load()
+    ops = importlib.import_module("tensorplay-mlu_amd.ops")
+    runtime = importlib.import_module("tensorplay-mlu_amd.runtime")
+    dev = importlib.import_module("tensorplay-mlu_amd.tensor").DeviceTensor
+    if not runtime.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+
+    log("bench: building config-2 inputs")
+    tensors = {F32: build_config2(ops, dev, F32), BF16: build_config2(ops, dev, BF16)}
+    tensors[F32]["out"] = ops.empty((N, N), F32)
+    plan = [(fn, factor * N * N * ESIZE[d]) for d, t in tensors.items()
+            for _, fn, factor in config2_ops(ops, t)]
+    step_bytes = sum(b for _, b in plan)
+
+    def step():
+        for fn, _ in plan:
+            fn()
+
+    log(f"bench: warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    runtime.synchronize()
+    ev = Events(lib)
+    log(f"bench: timing {args.steps} steps")
+    runtime.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    runtime.synchronize()
+    secs = time.perf_counter() - t0
+    value = step_bytes * args.steps / secs / 1e9
+
+    log("bench: dominant kernel")
+    roofline = dominant_kernel(lib, ev, tensors[F32])
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(secs / args.steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config2: broadcast elementwise, [8192,8192] fp32 and bf16 "
+                               "storage, row [8192] and column [8192,1] broadcasts, 26 operators "
+                               "per dtype (forward, in-place, scalar, unary, activation backward)",
+                   "shape": [N, N], "storage_dtypes": ["fp32", "bf16"],
+                   "bytes_per_step": step_bytes, "parallelism": "single GPU"},
+        "roofline": roofline,
+    }
+    if not args.no_suite:
+        log("bench: suite config 2")
+        suite = {"config2": suite_config2(ops, ev, tensors)}
+        del tensors
+        log("bench: suite config 3")
+        suite["config3"] = suite_config3(ops, dev, ev)
+        result["suite"] = suite
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,169 @@
+/* Thin kernel-level C-ABI of libtp_amd.so: one entry per device computation
+ * the reference delegates to a CNNL call.  These take raw device addresses,
+ * sizes and element strides, issue hand-written gfx950 HIP kernels on the
+ * device's single stream and return without waiting.  The host-side
+ * operator layer (tp_amd_ops.h) is built on these; they are exported so a
+ * caller can drive a kernel directly.
+ *
+ * ``device`` < 0 means the current device.  Every pointer must be device
+ * memory of that device (or NULL where stated).  Return codes as in
+ * tp_amd_types.h.
+ */
+#ifndef TP_AMD_KERNELS_H
+#define TP_AMD_KERNELS_H
+
+#include "tp_amd_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Binary operations (BinaryKernels.cpp:44-87). */
+typedef enum tp_amd_binary_op {
+    TP_AMD_BINARY_ADD = 0, /* out = a + alpha * b  (sub passes -alpha, :82) */
+    TP_AMD_BINARY_MUL = 1, /* out = a * b          (CNNL_OP_TENSOR_MUL) */
+    TP_AMD_BINARY_DIV = 2  /* out = a / b          (CNNL_DIV_TRUE, :60-61) */
+} tp_amd_binary_op;
+
+/* Replaces launch_binary's cnnlOpTensor / cnnlDiv_v3 (BinaryKernels.cpp:44-87).
+ * out[i] = a[i] op b[i] over the ``ndim``-d index space ``sizes``; each
+ * operand has its own element strides (0 for a broadcast dimension, the
+ * reference's padded descriptors :49-52).  a, b and out share ``dtype``
+ * (float32, float16 or bfloat16); arithmetic is float32, rounded once to
+ * ``dtype`` (compute type CNNL_DTYPE_FLOAT, :76).  ``out`` may alias ``a`` or
+ * ``b`` element for element (the in-place forms). */
+int tp_amd_launch_binary(int device, int op, int dtype, int ndim, const int64_t* sizes,
+                         const void* a, const int64_t* a_strides, const void* b,
+                         const int64_t* b_strides, void* out, const int64_t* out_strides,
+                         float alpha);
+
+/* Replaces affine's cnnlTransform_v2 (BinaryKernels.cpp:30-40): y = alpha * x
+ * + beta over ``n`` dense elements, float32 arithmetic, alpha and beta
+ * already rounded to float32 by the caller (:113-140, :189-248). */
+int tp_amd_launch_affine(int device, int dtype, int64_t n, const void* x, float alpha,
+                         float beta, void* y);
+
+/* Unary forward operations (UnaryKernels.cpp:106-214). */
+typedef enum tp_amd_unary_op {
+    TP_AMD_UNARY_EXP = 0,
+    TP_AMD_UNARY_LOG = 1,
+    TP_AMD_UNARY_SQRT = 2,
+    TP_AMD_UNARY_RSQRT = 3,
+    TP_AMD_UNARY_NEG = 4,
+    TP_AMD_UNARY_ABS = 5,
+    TP_AMD_UNARY_SQUARE = 6,   /* pow(x, 2) (cnnlSquare, :150) */
+    TP_AMD_UNARY_POW = 7,      /* pow(x, param) (cnnlPow, :176) */
+    TP_AMD_UNARY_RELU = 8,
+    TP_AMD_UNARY_SIGMOID = 9,
+    TP_AMD_UNARY_TANH = 10,
+    TP_AMD_UNARY_SILU = 11,
+    TP_AMD_UNARY_GELU = 12,      /* erf form, approximate="none" */
+    TP_AMD_UNARY_GELU_TANH = 13, /* tanh form, approximate="tanh" */
+    TP_AMD_UNARY_NUM_OPS = 14
+} tp_amd_unary_op;
+
+/* Replaces the CNNL unary and activation-forward calls
+ * (UnaryKernels.cpp:29-80, 106-214).  y (dense, row-major over ``sizes``) =
+ * f(x) with x read through ``x_strides``; float32 arithmetic rounded once to
+ * ``dtype``.  ``param`` is the exponent for TP_AMD_UNARY_POW. */
+int tp_amd_launch_unary(int device, int op, int dtype, int ndim, const int64_t* sizes,
+                        const void* x, const int64_t* x_strides, void* y, float param);
+
+/* Activation backward operations (UnaryKernels.cpp:83-104, 222-287). */
+typedef enum tp_amd_backward_op {
+    TP_AMD_BACKWARD_THRESHOLD = 0, /* dx = saved > param ? dy : 0, saved = input */
+    TP_AMD_BACKWARD_SIGMOID = 1,   /* dx = dy * y * (1 - y), saved = output */
+    TP_AMD_BACKWARD_TANH = 2,      /* dx = dy * (1 - y^2), saved = output */
+    TP_AMD_BACKWARD_GELU = 3,      /* dx = dy * (Phi(x) + x phi(x)), saved = input */
+    TP_AMD_BACKWARD_GELU_TANH = 4, /* derivative of the tanh form, saved = input */
+    TP_AMD_BACKWARD_SILU = 5       /* dx = dy * s * (1 + x (1 - s)), saved = input */
+} tp_amd_backward_op;
+
+/* Replaces cnnlThresholdBackward (UnaryKernels.cpp:239) and
+ * cnnlActivationBackward (:97).  All three arrays dense with ``n`` elements
+ * of ``dtype``; ``param`` is the threshold for TP_AMD_BACKWARD_THRESHOLD
+ * (already rounded to ``dtype`` by the caller, :229-236). */
+int tp_amd_launch_activation_backward(int device, int op, int dtype, int64_t n,
+                                      const void* grad, const void* saved, void* dx,
+                                      float param);
+
+/* Reductions (ReduceKernels.cpp:21-44, CNNL_REDUCE_ADD/AVG/MAX/MIN). */
+typedef enum tp_amd_reduce_op {
+    TP_AMD_REDUCE_SUM = 0,
+    TP_AMD_REDUCE_MEAN = 1,
+    TP_AMD_REDUCE_AMAX = 2,
+    TP_AMD_REDUCE_AMIN = 3
+} tp_amd_reduce_op;
+
+/* Replaces launch_reduce's cnnlReduce_v2 (ReduceKernels.cpp:21-44).  ``x`` is
+ * a dense [outer, r, inner] array of ``dtype``; out[o, i] = reduce over j of
+ * x[o, j, i], written dense [outer, inner] in ``dtype``.  float32 arithmetic;
+ * NaN inputs are skipped by amax/amin (CNNL_NOT_PROPAGATE_NAN, :33-36) and
+ * max(-0, +0) = +0, min(-0, +0) = -0, so the result does not depend on the
+ * order of evaluation.  r == 0 gives 0 for sum/mean. */
+int tp_amd_launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r,
+                         int64_t inner, const void* x, void* out);
+
+/* Replaces cnnlSoftmaxForward (ReduceKernels.cpp:171-183): x, y dense
+ * [outer, dim, inner] of ``dtype``; softmax (log_softmax when ``log``) along
+ * the middle axis, float32 arithmetic. */
+int tp_amd_launch_softmax(int device, int log, int dtype, int64_t outer, int64_t dim,
+                          int64_t inner, const void* x, void* y);
+
+/* Replaces cnnlSoftmaxBackward (ReduceKernels.cpp:185-199): from the forward
+ * output y and the upstream gradient dy, dx = y * (dy - sum(dy * y)) for
+ * softmax, dx = dy - exp(y) * sum(dy) for log_softmax (sums along the
+ * middle axis).  All dense [outer, dim, inner] of ``dtype``. */
+int tp_amd_launch_softmax_backward(int device, int log, int dtype, int64_t outer,
+                                   int64_t dim, int64_t inner, const void* y,
+                                   const void* dy, void* dx);
+
+/* Replaces cnnlMatMul_v2 / cnnlStrideBatchMatMul_v3 (BlasKernels.cpp:202-242).
+ * For each of ``batch`` problems:
+ *   C[b] (M x N, row stride ldc) = alpha * op(A[b]) op(B[b]) + beta * Cin[b]
+ * op(A) is M x K: A stored row-major M x K (lda >= K) or, when trans_a, the
+ * transpose of a row-major K x M matrix (lda >= M) -- read in place, never
+ * copied (as_operand, :38-54).  op(B) likewise K x N from a row-major K x N
+ * (ldb >= N) or, when trans_b, a row-major N x K (ldb >= K).  Batch strides
+ * are in elements; 0 repeats one matrix for every batch (:221-222).  ``cin``
+ * (may be NULL when beta == 0, may equal ``c``) is read at
+ * cin[b * cin_stride_b + i * cin_rs + j * cin_cs], so a bias row broadcast
+ * over M is cin_rs = 0, cin_cs = 1.  dtype float32, float16 or bfloat16;
+ * accumulation in float32 (CNNL_DTYPE_FLOAT compute, :113,159), result
+ * rounded once to ``dtype``; float32 inputs are multiplied in full float32
+ * (no reduced-precision mode; gfx950 has no TF32 matrix instruction). */
+int tp_amd_launch_gemm(int device, int dtype, int64_t batch, int64_t m, int64_t n,
+                       int64_t k, float alpha, const void* a, int64_t lda, int64_t stride_a,
+                       int trans_a, const void* b, int64_t ldb, int64_t stride_b, int trans_b,
+                       float beta, const void* cin, int64_t cin_rs, int64_t cin_cs,
+                       int64_t cin_stride_b, void* c, int64_t ldc, int64_t stride_c);
+
+/* Replaces cnnlCastDataType (CopyKernels.cpp:125-139): ``n`` dense elements
+ * converted from ``src_dtype`` to ``dst_dtype``.  Float to narrower float
+ * rounds to nearest even (NaN stays NaN, overflow gives infinity); float to
+ * integer truncates toward zero; anything to bool is (x != 0); integer to
+ * float rounds to nearest even.  Any pair of the ten dtypes is accepted. */
+int tp_amd_launch_cast(int device, int src_dtype, int dst_dtype, int64_t n, const void* src,
+                       void* dst);
+
+/* Replaces cnnlFill_v3 (CopyKernels.cpp:266-299): every element of the
+ * strided view (sizes/strides over ``ndim`` dims) set to the ``elem_size``
+ * bytes at ``value`` (1, 2, 4 or 8 bytes; the caller encodes the value per
+ * dtype, :272-283). */
+int tp_amd_launch_fill(int device, int elem_size, const void* value, int ndim,
+                       const int64_t* sizes, void* dst, const int64_t* dst_strides);
+
+/* Replaces strided_copy's cnnlCopy_v2 / memcpy fast path
+ * (Cnnl.cpp:127-176): dst[idx] = src[idx] over ``sizes`` for elements of
+ * ``elem_size`` bytes, each side with its own strides (src strides may be 0
+ * for an expanded view).  Dimensions laid out back to back in both are
+ * merged first; a dense-to-dense copy is one device memcpy. */
+int tp_amd_launch_strided_copy(int device, int elem_size, int ndim, const int64_t* sizes,
+                               void* dst, const int64_t* dst_strides, const void* src,
+                               const int64_t* src_strides);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TP_AMD_KERNELS_H */

@@ -1,0 +1,103 @@
+/* Runtime, device hooks and caching allocator of libtp_amd.so.
+ *
+ * Each entry states the reference interface it replaces.  The five
+ * ``tp_mlu_*`` entries keep the reference's exact names and signatures
+ * (tensorplay_mlu/csrc/Module.cpp:15-37, bound by ctypes in
+ * tensorplay_mlu/__init__.py:73-76) so the reference's Python loader binds
+ * this library unchanged; everything else is ``tp_amd_*``.
+ *
+ * Ordering: every device has exactly one HIP stream (default priority,
+ * non-blocking) and every kernel, device-to-device copy and allocator reuse
+ * is ordered on it, as the reference orders everything on one CNRT queue per
+ * device (MLURuntime.cpp:81-93, MLUAllocator.cpp:1-6).
+ */
+#ifndef TP_AMD_RUNTIME_H
+#define TP_AMD_RUNTIME_H
+
+#include "tp_amd_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- C entry points with the reference's names (Module.cpp:15-37) ------ */
+
+/* Replaces tp_mlu_init (Module.cpp:15-22).  Initialises the runtime and
+ * allocator; returns 0 on success, 1 on failure (the reference's codes).
+ * Registering TensorPlay's host fallbacks is done by the TensorPlay adapter
+ * (csrc/tensorplay/Module.cpp), which wraps this call. */
+int tp_mlu_init(void);
+
+/* Replaces tp_mlu_device_count (Module.cpp:24, MLURuntime.cpp:34-41):
+ * visible devices, 0 when no driver or GPU is present. */
+int tp_mlu_device_count(void);
+
+/* Replaces tp_mlu_memory_stats (Module.cpp:27-33): out[0..3] = allocated,
+ * reserved, peak allocated, peak reserved bytes of device ``index``. */
+void tp_mlu_memory_stats(int index, int64_t* out);
+
+/* Replaces tp_mlu_reset_peak_memory_stats (Module.cpp:35). */
+void tp_mlu_reset_peak_memory_stats(int index);
+
+/* Replaces tp_mlu_empty_cache (Module.cpp:37, MLUAllocator.cpp:208-219):
+ * synchronizes each device's stream, then returns cached unused blocks. */
+void tp_mlu_empty_cache(void);
+
+/* Replaces tp_mlu_last_error (bound at tensorplay_mlu/__init__.py:77):
+ * the calling thread's last error message ("" when none). */
+const char* tp_mlu_last_error(void);
+
+/* ---- device hooks (MLUHooks.cpp:14-52, MLURuntime.cpp:43-136) ---------- */
+
+/* PrivateUse1HooksInterface::is_available (MLUHooks.cpp:15). */
+int tp_amd_is_available(void);
+/* current_device / set_device (MLUHooks.cpp:17-18, MLURuntime.cpp:43-54). */
+int tp_amd_current_device(int* index);
+int tp_amd_set_device(int index);
+/* synchronize (MLUHooks.cpp:19-21, MLURuntime.cpp:107-110): waits for the
+ * device's stream; index < 0 means the current device. */
+int tp_amd_synchronize(int index);
+/* memory_info (MLUHooks.cpp:46-51): free and total bytes from the driver. */
+int tp_amd_mem_get_info(int index, size_t* free_bytes, size_t* total_bytes);
+/* copy_bytes (MLUHooks.cpp:23-44): device -1 is host memory.  Host copies
+ * return once the bytes have landed (MLURuntime.cpp:112-129); a copy on one
+ * device is ordered on its stream; between two devices it bounces through
+ * the host. */
+int tp_amd_copy_bytes(void* dst, int dst_device, const void* src, int src_device,
+                      size_t nbytes);
+/* The device's single stream as an opaque handle (hipStream_t), for callers
+ * that need to order their own work with this library's
+ * (MLURuntime.cpp:81-93 queue()). */
+int tp_amd_stream(int index, void** stream);
+
+/* ---- caching allocator (MLUAllocator.cpp:61-236) ------------------------ */
+
+/* Allocator::allocate (MLUAllocator.cpp:63-73, take :98-128): a block of at
+ * least ``nbytes`` on ``device`` (< 0: current).  ``*ptr`` is its address,
+ * ``*ctx`` the handle tp_amd_free takes (both NULL for nbytes == 0).  Sizes
+ * round up to 512 B below 1 MiB and to 2 MiB above; a cached block is reused
+ * when it is no more than a quarter larger than the rounded request; on
+ * out-of-memory the cache is released and the allocation retried once. */
+int tp_amd_malloc(size_t nbytes, int device, void** ptr, void** ctx);
+/* The DataPtr deleter (MLUAllocator.cpp:93-96, give_back :130-141): the
+ * block returns to its device's pool for reuse by later work on the same
+ * stream.  NULL is ignored. */
+void tp_amd_free(void* ctx);
+/* Size in bytes of the block behind ``ctx`` (after rounding). */
+size_t tp_amd_block_size(void* ctx);
+
+/* ---- timing on the device's stream (hipEvent pairs) --------------------- */
+
+/* Events recorded on the device's single stream, so a measurement brackets
+ * exactly this library's kernels (reference counterpart: the notifier pair
+ * of MLUProfiler.cpp:20-51). */
+int tp_amd_event_create(void** event);
+int tp_amd_event_record(void* event, int device);
+int tp_amd_event_elapsed_ms(void* start, void* stop, float* ms);
+int tp_amd_event_destroy(void* event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TP_AMD_RUNTIME_H */

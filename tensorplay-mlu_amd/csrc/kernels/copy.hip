@@ -1,0 +1,377 @@
+// Fill, dtype conversion and strided copy kernels for gfx950.
+//
+// * Fill writes 16-byte packets of the replicated element pattern when the
+//   view is dense, the strided kernel otherwise.
+// * Conversion covers every pair of the ten dtypes; each thread converts
+//   kPerThread elements with coalesced accesses.  Float to narrower float
+//   rounds to nearest even, float to integer truncates toward zero
+//   (saturating to int64, NaN to 0) and wraps to the target width, anything
+//   to bool is x != 0.
+// * Strided copy merges dimensions first; a dense copy is one device memcpy,
+//   a 2-D transpose goes through a padded LDS tile so both the read and the
+//   write side are coalesced, anything else takes the general kernel.
+
+#include <cstring>
+
+#include "device_common.h"
+#include "layout.h"
+#include "../runtime.h"
+#include "tp_amd_kernels.h"
+
+namespace tp_amd {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int BYTES>
+struct Raw;
+template <>
+struct Raw<1> { using type = uint8_t; };
+template <>
+struct Raw<2> { using type = uint16_t; };
+template <>
+struct Raw<4> { using type = uint32_t; };
+template <>
+struct Raw<8> { using type = uint64_t; };
+
+int64_t grid_for(int64_t work, int64_t per_block, int device) {
+    int64_t blocks = (work + per_block - 1) / per_block;
+    const int64_t cap = static_cast<int64_t>(cu_count(device)) * 64;
+    if (blocks > cap) blocks = cap;
+    return blocks > 0 ? blocks : 1;
+}
+
+// ---- fill --------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void fill_dense_kernel(uint4* dst, int64_t npackets,
+                                                            uint4 pattern) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < npackets;
+         i += stride) {
+        dst[i] = pattern;
+    }
+}
+
+template <typename R>
+__global__ __launch_bounds__(kBlock) void fill_nd_kernel(NdParams<1> p, R* dst, int64_t n,
+                                                         R value) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += stride) {
+        int64_t rem = i, off = 0;
+        for (int d = p.ndim - 1; d >= 0; --d) {
+            const int64_t q = rem / p.sizes[d];
+            off += (rem - q * p.sizes[d]) * p.strides[0][d];
+            rem = q;
+        }
+        dst[off] = value;
+    }
+}
+
+template <typename R>
+void fill_typed(int device, const void* value, int ndim, const int64_t* sizes, void* dst,
+                const int64_t* strides) {
+    R v;
+    std::memcpy(&v, value, sizeof(R));
+    const int64_t* s[1] = {strides};
+    const Layout<1> l = coalesce<1>(ndim, sizes, s);
+    const int64_t n = l.numel();
+    if (n == 0) return;
+    hipStream_t st = stream(device);
+    const bool dense = l.ndim == 0 || (l.ndim == 1 && l.strides[0][0] == 1);
+    if (dense && aligned16(dst)) {
+        uint4 pattern;
+        R rep[16 / sizeof(R)];
+        for (auto& r : rep) r = v;
+        std::memcpy(&pattern, rep, 16);
+        const int64_t npackets = n * static_cast<int64_t>(sizeof(R)) / 16;
+        if (npackets > 0) {
+            fill_dense_kernel<<<grid_for(npackets, kBlock * 4, device), kBlock, 0, st>>>(
+                static_cast<uint4*>(dst), npackets, pattern);
+            TP_AMD_HIP_CHECK(hipGetLastError());
+        }
+        const int64_t done = npackets * 16 / static_cast<int64_t>(sizeof(R));
+        if (done < n) {
+            Layout<1> tail;
+            tail.ndim = 1;
+            tail.sizes[0] = n - done;
+            tail.strides[0][0] = 1;
+            fill_nd_kernel<R><<<1, kBlock, 0, st>>>(nd_params(tail), static_cast<R*>(dst) + done,
+                                                    n - done, v);
+            TP_AMD_HIP_CHECK(hipGetLastError());
+        }
+        return;
+    }
+    fill_nd_kernel<R><<<grid_for(n, kBlock * 4, device), kBlock, 0, st>>>(
+        nd_params(l), static_cast<R*>(dst), n, v);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+// ---- conversion ----------------------------------------------------------
+
+// Device element types by dtype code.
+struct F32 { using S = float; };
+struct F16 { using S = uint16_t; };
+struct BF16 { using S = uint16_t; };
+struct F64 { using S = double; };
+struct I8 { using S = int8_t; };
+struct I16 { using S = int16_t; };
+struct I32 { using S = int32_t; };
+struct I64 { using S = int64_t; };
+struct U8 { using S = uint8_t; };
+struct B1 { using S = uint8_t; };
+
+template <typename D>
+constexpr bool is_float_tag() {
+    return std::is_same<D, F32>::value || std::is_same<D, F16>::value ||
+           std::is_same<D, BF16>::value || std::is_same<D, F64>::value;
+}
+
+// Read an element as either a double (float sources) or an int64 (integer
+// and bool sources).  float16 and bfloat16 widen exactly.
+template <typename D>
+__device__ __forceinline__ double read_float(typename D::S v) {
+    if constexpr (std::is_same<D, F16>::value) return f16_to_float(v);
+    else if constexpr (std::is_same<D, BF16>::value) return bf16_to_float(v);
+    else return static_cast<double>(v);
+}
+
+template <typename D>
+__device__ __forceinline__ typename D::S write_from_float(double x) {
+    if constexpr (std::is_same<D, F64>::value) {
+        return x;
+    } else if constexpr (std::is_same<D, F32>::value) {
+        return static_cast<float>(x);
+    } else if constexpr (std::is_same<D, F16>::value) {
+        // Through float32: the source is float32 or narrower except for
+        // float64 sources, which the operator layer routes through float32.
+        return float_to_f16(static_cast<float>(x));
+    } else if constexpr (std::is_same<D, BF16>::value) {
+        return float_to_bf16(static_cast<float>(x));
+    } else if constexpr (std::is_same<D, B1>::value) {
+        return static_cast<uint8_t>(x != 0.0 ? 1 : 0);
+    } else {
+        // Truncate toward zero into int64 (saturating, NaN -> 0), then wrap.
+        int64_t t;
+        if (!(x == x)) t = 0;
+        else if (x >= 9223372036854775807.0) t = INT64_MAX;
+        else if (x <= -9223372036854775808.0) t = INT64_MIN;
+        else t = static_cast<int64_t>(x);
+        return static_cast<typename D::S>(t);
+    }
+}
+
+template <typename D>
+__device__ __forceinline__ typename D::S write_from_int(int64_t x) {
+    if constexpr (std::is_same<D, F64>::value) return static_cast<double>(x);
+    else if constexpr (std::is_same<D, F32>::value) return static_cast<float>(x);
+    else if constexpr (std::is_same<D, F16>::value) return float_to_f16(static_cast<float>(x));
+    else if constexpr (std::is_same<D, BF16>::value) return float_to_bf16(static_cast<float>(x));
+    else if constexpr (std::is_same<D, B1>::value) return static_cast<uint8_t>(x != 0 ? 1 : 0);
+    else return static_cast<typename D::S>(x);
+}
+
+// float32 -> float16 / bfloat16 directly from a float (the hot casts).
+template <typename Src, typename Dst>
+__device__ __forceinline__ typename Dst::S convert(typename Src::S v) {
+    if constexpr (std::is_same<Src, Dst>::value && !std::is_same<Src, B1>::value) {
+        return v;
+    } else if constexpr (std::is_same<Src, F32>::value && std::is_same<Dst, BF16>::value) {
+        return float_to_bf16(v);
+    } else if constexpr (std::is_same<Src, F32>::value && std::is_same<Dst, F16>::value) {
+        return float_to_f16(v);
+    } else if constexpr (std::is_same<Src, B1>::value) {
+        return write_from_int<Dst>(v != 0 ? 1 : 0);
+    } else if constexpr (is_float_tag<Src>()) {
+        return write_from_float<Dst>(read_float<Src>(v));
+    } else {
+        return write_from_int<Dst>(static_cast<int64_t>(v));
+    }
+}
+
+constexpr int kPerThread = 8;
+
+template <typename Src, typename Dst>
+__global__ __launch_bounds__(kBlock) void cast_kernel(const typename Src::S* src,
+                                                      typename Dst::S* dst, int64_t n) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kBlock * kPerThread) + threadIdx.x;
+    typename Src::S v[kPerThread];
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+        const int64_t i = base + k * kBlock;
+        if (i < n) v[k] = src[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+        const int64_t i = base + k * kBlock;
+        if (i < n) dst[i] = convert<Src, Dst>(v[k]);
+    }
+}
+
+template <typename Src, typename Dst>
+void cast_typed(int device, int64_t n, const void* src, void* dst) {
+    const int64_t per_block = static_cast<int64_t>(kBlock) * kPerThread;
+    const int64_t blocks = (n + per_block - 1) / per_block;
+    cast_kernel<Src, Dst><<<blocks, kBlock, 0, stream(device)>>>(
+        static_cast<const typename Src::S*>(src), static_cast<typename Dst::S*>(dst), n);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+template <typename Src>
+void cast_from(int device, int dst_dtype, int64_t n, const void* src, void* dst) {
+    switch (dst_dtype) {
+        case TP_AMD_FLOAT32: cast_typed<Src, F32>(device, n, src, dst); break;
+        case TP_AMD_FLOAT16: cast_typed<Src, F16>(device, n, src, dst); break;
+        case TP_AMD_BFLOAT16: cast_typed<Src, BF16>(device, n, src, dst); break;
+        case TP_AMD_FLOAT64: cast_typed<Src, F64>(device, n, src, dst); break;
+        case TP_AMD_INT8: cast_typed<Src, I8>(device, n, src, dst); break;
+        case TP_AMD_INT16: cast_typed<Src, I16>(device, n, src, dst); break;
+        case TP_AMD_INT32: cast_typed<Src, I32>(device, n, src, dst); break;
+        case TP_AMD_INT64: cast_typed<Src, I64>(device, n, src, dst); break;
+        case TP_AMD_UINT8: cast_typed<Src, U8>(device, n, src, dst); break;
+        case TP_AMD_BOOL: cast_typed<Src, B1>(device, n, src, dst); break;
+        default: TP_AMD_CHECK(false, "unknown destination dtype ", dst_dtype);
+    }
+}
+
+// ---- strided copy ------------------------------------------------------------
+
+template <typename R>
+__global__ __launch_bounds__(kBlock) void copy_nd_kernel(NdParams<2> p, R* dst, const R* src,
+                                                         int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += stride) {
+        int64_t rem = i, od = 0, os = 0;
+        for (int d = p.ndim - 1; d >= 0; --d) {
+            const int64_t q = rem / p.sizes[d];
+            const int64_t idx = rem - q * p.sizes[d];
+            od += idx * p.strides[0][d];
+            os += idx * p.strides[1][d];
+            rem = q;
+        }
+        dst[od] = src[os];
+    }
+}
+
+// dst[r, c] (row stride ld_dst, unit column stride) = src[r, c] read with
+// unit row stride and column stride ld_src: a transpose.  64x64 tiles staged
+// through LDS with one element of padding per row.
+constexpr int kTile = 64;
+
+template <typename R>
+__global__ __launch_bounds__(kBlock) void transpose_kernel(R* dst, const R* src, int64_t rows,
+                                                           int64_t cols, int64_t ld_dst,
+                                                           int64_t ld_src) {
+    __shared__ R tile[kTile][kTile + 1];
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTile;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kTile;
+    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;  // 64 x 4
+    // Read: consecutive threads walk r (the source's unit-stride axis).
+    for (int j = ty; j < kTile; j += kBlock / kTile) {
+        const int64_t r = r0 + tx, c = c0 + j;
+        if (r < rows && c < cols) tile[j][tx] = src[c * ld_src + r];
+    }
+    __syncthreads();
+    // Write: consecutive threads walk c (the destination's unit-stride axis).
+    for (int j = ty; j < kTile; j += kBlock / kTile) {
+        const int64_t r = r0 + j, c = c0 + tx;
+        if (r < rows && c < cols) dst[r * ld_dst + c] = tile[tx][j];
+    }
+}
+
+template <typename R>
+void copy_typed(int device, const Layout<2>& l, void* dst, const void* src) {
+    const int64_t n = l.numel();
+    hipStream_t st = stream(device);
+    if (l.ndim == 2 && l.strides[0][1] == 1 && l.strides[1][0] == 1 &&
+        l.strides[0][0] >= l.sizes[1] && l.strides[1][1] >= l.sizes[0]) {
+        const dim3 grid(static_cast<unsigned>((l.sizes[1] + kTile - 1) / kTile),
+                        static_cast<unsigned>((l.sizes[0] + kTile - 1) / kTile));
+        if (grid.y < 65536u) {
+            transpose_kernel<R><<<grid, kBlock, 0, st>>>(static_cast<R*>(dst),
+                                                         static_cast<const R*>(src), l.sizes[0],
+                                                         l.sizes[1], l.strides[0][0],
+                                                         l.strides[1][1]);
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            return;
+        }
+    }
+    copy_nd_kernel<R><<<grid_for(n, kBlock * 4, device), kBlock, 0, st>>>(
+        nd_params(l), static_cast<R*>(dst), static_cast<const R*>(src), n);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+}  // namespace tp_amd
+
+using namespace tp_amd;
+
+extern "C" {
+
+int tp_amd_launch_fill(int device, int elem_size, const void* value, int ndim,
+                       const int64_t* sizes, void* dst, const int64_t* dst_strides) {
+    return guarded([&] {
+        TP_AMD_CHECK(value != nullptr, "tp_amd_launch_fill: null value");
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        switch (elem_size) {
+            case 1: fill_typed<uint8_t>(index, value, ndim, sizes, dst, dst_strides); break;
+            case 2: fill_typed<uint16_t>(index, value, ndim, sizes, dst, dst_strides); break;
+            case 4: fill_typed<uint32_t>(index, value, ndim, sizes, dst, dst_strides); break;
+            case 8: fill_typed<uint64_t>(index, value, ndim, sizes, dst, dst_strides); break;
+            default: TP_AMD_CHECK(false, "fill: element size ", elem_size, " not 1/2/4/8");
+        }
+    });
+}
+
+int tp_amd_launch_cast(int device, int src_dtype, int dst_dtype, int64_t n, const void* src,
+                       void* dst) {
+    return guarded([&] {
+        TP_AMD_CHECK(n >= 0, "negative element count");
+        if (n == 0) return;
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        switch (src_dtype) {
+            case TP_AMD_FLOAT32: cast_from<F32>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_FLOAT16: cast_from<F16>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_BFLOAT16: cast_from<BF16>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_FLOAT64: cast_from<F64>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_INT8: cast_from<I8>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_INT16: cast_from<I16>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_INT32: cast_from<I32>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_INT64: cast_from<I64>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_UINT8: cast_from<U8>(index, dst_dtype, n, src, dst); break;
+            case TP_AMD_BOOL: cast_from<B1>(index, dst_dtype, n, src, dst); break;
+            default: TP_AMD_CHECK(false, "unknown source dtype ", src_dtype);
+        }
+    });
+}
+
+int tp_amd_launch_strided_copy(int device, int elem_size, int ndim, const int64_t* sizes,
+                               void* dst, const int64_t* dst_strides, const void* src,
+                               const int64_t* src_strides) {
+    return guarded([&] {
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        const int64_t* s[2] = {dst_strides, src_strides};
+        const Layout<2> l = coalesce<2>(ndim, sizes, s);
+        const int64_t n = l.numel();
+        if (n == 0) return;
+        if (l.ndim == 0 || (l.ndim == 1 && l.strides[0][0] == 1 && l.strides[1][0] == 1)) {
+            copy_on_device(dst, src, static_cast<size_t>(n) * elem_size, index);
+            return;
+        }
+        switch (elem_size) {
+            case 1: copy_typed<uint8_t>(index, l, dst, src); break;
+            case 2: copy_typed<uint16_t>(index, l, dst, src); break;
+            case 4: copy_typed<uint32_t>(index, l, dst, src); break;
+            case 8: copy_typed<uint64_t>(index, l, dst, src); break;
+            default: TP_AMD_CHECK(false, "copy: element size ", elem_size, " not 1/2/4/8");
+        }
+    });
+}
+
+}  // extern "C"

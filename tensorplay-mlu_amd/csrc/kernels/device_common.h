@@ -1,0 +1,150 @@
+// Device-side building blocks shared by the gfx950 kernels: element
+// conversions (float32 compute, round-to-nearest-even stores), 16-byte
+// vector packets, and magic-number division for index math.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tp_amd {
+
+// Storage types.  bfloat16 and float16 are carried as raw 16-bit patterns
+// and converted explicitly, so rounding is exactly round-to-nearest-even
+// with NaN kept quiet, independent of compiler defaults.
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_float(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t float_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_float(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return static_cast<float>(v);
+}
+
+__device__ __forceinline__ uint16_t float_to_f16(float f) {
+    // v_cvt_f16_f32 rounds to nearest even (the default round mode).
+    _Float16 v = static_cast<_Float16>(f);
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+    using storage = float;
+    __device__ __forceinline__ static float load(float v) { return v; }
+    __device__ __forceinline__ static float store(float f) { return f; }
+};
+template <>
+struct Elem<bf16_t> {
+    using storage = uint16_t;
+    __device__ __forceinline__ static float load(uint16_t v) { return bf16_to_float(v); }
+    __device__ __forceinline__ static uint16_t store(float f) { return float_to_bf16(f); }
+};
+template <>
+struct Elem<f16_t> {
+    using storage = uint16_t;
+    __device__ __forceinline__ static float load(uint16_t v) { return f16_to_float(v); }
+    __device__ __forceinline__ static uint16_t store(float f) { return float_to_f16(f); }
+};
+
+// A 16-byte packet of N = 16 / sizeof(storage) elements.
+template <typename T>
+struct Packet {
+    using S = typename Elem<T>::storage;
+    static constexpr int N = 16 / sizeof(S);
+    S v[N];
+};
+
+template <typename T>
+__device__ __forceinline__ Packet<T> load_packet(const typename Elem<T>::storage* p) {
+    Packet<T> out;
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    __builtin_memcpy(&out, &raw, 16);
+    return out;
+}
+
+template <typename T>
+__device__ __forceinline__ void store_packet(typename Elem<T>::storage* p, const Packet<T>& v) {
+    uint4 raw;
+    __builtin_memcpy(&raw, &v, 16);
+    *reinterpret_cast<uint4*>(p) = raw;
+}
+
+// Streaming variants: the data is touched once, so keep it out of the
+// caches' way (nontemporal loads/stores).
+template <typename T>
+__device__ __forceinline__ Packet<T> load_packet_nt(const typename Elem<T>::storage* p) {
+    Packet<T> out;
+    uint4 raw;
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+    raw.x = __builtin_nontemporal_load(&q->x);
+    raw.y = __builtin_nontemporal_load(&q->y);
+    raw.z = __builtin_nontemporal_load(&q->z);
+    raw.w = __builtin_nontemporal_load(&q->w);
+    __builtin_memcpy(&out, &raw, 16);
+    return out;
+}
+
+template <typename T>
+__device__ __forceinline__ void store_packet_nt(typename Elem<T>::storage* p, const Packet<T>& v) {
+    uint4 raw;
+    __builtin_memcpy(&raw, &v, 16);
+    uint4* q = reinterpret_cast<uint4*>(p);
+    __builtin_nontemporal_store(raw.x, &q->x);
+    __builtin_nontemporal_store(raw.y, &q->y);
+    __builtin_nontemporal_store(raw.z, &q->z);
+    __builtin_nontemporal_store(raw.w, &q->w);
+}
+
+// Unsigned division by a runtime constant d (1 <= d < 2^31) for numerators
+// n < 2^31: with s = ceil(log2 d) and m = ceil(2^(31+s) / d) (which fits in
+// 32 bits), floor(n / d) = (n * m) >> (31 + s).  The rounding error of m
+// adds less than n / 2^(31+s) < 2^-s <= 1/d to n/d, which cannot carry
+// floor(n/d) to the next integer.
+struct FastDiv {
+    uint32_t d;
+    uint32_t m;
+    uint32_t shift;  // 31 + s
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    const uint64_t m = ((uint64_t(1) << (31 + s)) + d - 1) / d;
+    return FastDiv{d, static_cast<uint32_t>(m), 31 + s};
+}
+
+__device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv& f) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.shift);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Wavefront size on gfx9 / CDNA.
+constexpr int kWave = 64;
+
+template <typename T>
+__device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
+    return __shfl_xor(v, mask, kWave);
+}
+
+}  // namespace tp_amd

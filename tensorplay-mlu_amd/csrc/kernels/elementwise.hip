@@ -1,0 +1,428 @@
+// Elementwise kernels for gfx950: broadcasting binary arithmetic, the
+// affine transform behind the scalar forms, unary math and activations, and
+// the activation backward kernels.
+//
+// Streaming design (HBM-bound): every thread moves 16-byte packets (4 fp32 or
+// 8 bf16/fp16), issues all of its loads before any arithmetic so several
+// packets per thread are in flight, and one block covers a contiguous span of
+// kUnroll * 256 packets so a wavefront's accesses are fully coalesced.  After
+// coalescing, broadcasting reduces to a 2-D [R, C] index space in which each
+// operand is full, a row broadcast (b[c]), a column broadcast (b[r]) or a
+// scalar; anything else takes the general strided kernel.
+
+#include "device_common.h"
+#include "layout.h"
+#include "math_ops.h"
+#include "../runtime.h"
+#include "tp_amd_kernels.h"
+
+namespace tp_amd {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+#define TP_AMD_DISPATCH_FLOAT(dtype, T, ...)                                      \
+    switch (dtype) {                                                              \
+        case TP_AMD_FLOAT32: { using T = float; __VA_ARGS__; break; }             \
+        case TP_AMD_BFLOAT16: { using T = bf16_t; __VA_ARGS__; break; }           \
+        case TP_AMD_FLOAT16: { using T = f16_t; __VA_ARGS__; break; }             \
+        default: TP_AMD_CHECK(false, "elementwise kernels take float32, float16 or " \
+                              "bfloat16, got ", dtype_name(dtype));               \
+    }
+
+// ---- dense kernels: NIN inputs, one output, all contiguous ---------------
+
+template <typename T, int NIN, typename F>
+__global__ __launch_bounds__(kBlock) void flat_kernel(const typename Elem<T>::storage* in0,
+                                                      const typename Elem<T>::storage* in1,
+                                                      typename Elem<T>::storage* out,
+                                                      int64_t npackets, int64_t n, F f) {
+    constexpr int N = Packet<T>::N;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+    Packet<T> x0[kUnroll], x1[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t p = base + k * kBlock;
+        if (p < npackets) {
+            x0[k] = load_packet_nt<T>(in0 + p * N);
+            if constexpr (NIN == 2) x1[k] = load_packet_nt<T>(in1 + p * N);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t p = base + k * kBlock;
+        if (p < npackets) {
+            Packet<T> y;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float v;
+                if constexpr (NIN == 1) v = f(Elem<T>::load(x0[k].v[j]));
+                else v = f(Elem<T>::load(x0[k].v[j]), Elem<T>::load(x1[k].v[j]));
+                y.v[j] = Elem<T>::store(v);
+            }
+            store_packet_nt<T>(out + p * N, y);
+        }
+    }
+    // The n % N trailing elements, one per thread of block 0.
+    if (blockIdx.x == 0) {
+        const int64_t i = npackets * N + threadIdx.x;
+        if (i < n) {
+            float v;
+            if constexpr (NIN == 1) v = f(Elem<T>::load(in0[i]));
+            else v = f(Elem<T>::load(in0[i]), Elem<T>::load(in1[i]));
+            out[i] = Elem<T>::store(v);
+        }
+    }
+}
+
+// ---- broadcasting binary over [R, C] ---------------------------------------
+
+enum Mode { kFull = 0, kRowB = 1, kColB = 2, kScal = 3 };
+
+template <typename T, int MODE, bool BIG>
+__device__ __forceinline__ Packet<T> fetch(const typename Elem<T>::storage* x, int64_t i,
+                                           int64_t r, int64_t c) {
+    if constexpr (MODE == kFull) {
+        return load_packet_nt<T>(x + i);
+    } else if constexpr (MODE == kRowB) {
+        return load_packet<T>(x + c);
+    } else {
+        const typename Elem<T>::storage s = MODE == kColB ? x[r] : x[0];
+        Packet<T> p;
+#pragma unroll
+        for (int j = 0; j < Packet<T>::N; ++j) p.v[j] = s;
+        return p;
+    }
+}
+
+// C % N == 0, so a packet never crosses a row.  BIG selects 64-bit index
+// math for index spaces of 2^31 elements or more.
+template <typename T, int MA, int MB, bool BIG, typename F>
+__global__ __launch_bounds__(kBlock) void binary2d_kernel(const typename Elem<T>::storage* a,
+                                                          const typename Elem<T>::storage* b,
+                                                          typename Elem<T>::storage* out,
+                                                          int64_t npackets, int64_t C,
+                                                          FastDiv cdiv, F f) {
+    constexpr int N = Packet<T>::N;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+    Packet<T> xa[kUnroll], xb[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t p = base + k * kBlock;
+        if (p < npackets) {
+            const int64_t i = p * N;
+            int64_t r, c;
+            if constexpr (BIG) {
+                r = i / C;
+            } else {
+                r = fastdiv(static_cast<uint32_t>(i), cdiv);
+            }
+            c = i - r * C;
+            xa[k] = fetch<T, MA, BIG>(a, i, r, c);
+            xb[k] = fetch<T, MB, BIG>(b, i, r, c);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t p = base + k * kBlock;
+        if (p < npackets) {
+            Packet<T> y;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                y.v[j] = Elem<T>::store(f(Elem<T>::load(xa[k].v[j]), Elem<T>::load(xb[k].v[j])));
+            }
+            store_packet_nt<T>(out + p * N, y);
+        }
+    }
+}
+
+// ---- general strided index space --------------------------------------------
+
+// Operand 0 is the output; operands 1..NIN the inputs.
+template <typename T, int NIN, typename F>
+__global__ __launch_bounds__(kBlock) void nd_kernel(NdParams<NIN + 1> p,
+                                                    typename Elem<T>::storage* out,
+                                                    const typename Elem<T>::storage* in0,
+                                                    const typename Elem<T>::storage* in1,
+                                                    int64_t n, F f) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += stride) {
+        int64_t rem = i;
+        int64_t off[NIN + 1] = {};
+        for (int d = p.ndim - 1; d >= 0; --d) {
+            const int64_t size = p.sizes[d];
+            const int64_t q = rem / size;
+            const int64_t idx = rem - q * size;
+            rem = q;
+#pragma unroll
+            for (int k = 0; k <= NIN; ++k) off[k] += idx * p.strides[k][d];
+        }
+        float v;
+        if constexpr (NIN == 1) v = f(Elem<T>::load(in0[off[1]]));
+        else v = f(Elem<T>::load(in0[off[1]]), Elem<T>::load(in1[off[2]]));
+        out[off[0]] = Elem<T>::store(v);
+    }
+}
+
+int64_t flat_grid(int64_t npackets) {
+    const int64_t per_block = static_cast<int64_t>(kBlock) * kUnroll;
+    const int64_t blocks = (npackets + per_block - 1) / per_block;
+    return blocks > 0 ? blocks : 1;
+}
+
+int64_t nd_grid(int64_t n, int device) {
+    const int64_t want = (n + kBlock - 1) / kBlock;
+    const int64_t cap = static_cast<int64_t>(cu_count(device)) * 32;
+    return want < cap ? (want > 0 ? want : 1) : cap;
+}
+
+template <typename T, int NIN, typename F>
+void launch_flat(int device, const void* in0, const void* in1, void* out, int64_t n, F f) {
+    using S = typename Elem<T>::storage;
+    constexpr int N = Packet<T>::N;
+    const bool vec = aligned16(in0) && aligned16(out) && (NIN == 1 || aligned16(in1));
+    const int64_t npackets = vec ? n / N : 0;
+    if (!vec) {
+        // Unaligned views: the general kernel over one dense dimension.
+        Layout<NIN + 1> l;
+        l.ndim = 1;
+        l.sizes[0] = n;
+        for (int k = 0; k <= NIN; ++k) l.strides[k][0] = 1;
+        nd_kernel<T, NIN, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
+            nd_params(l), static_cast<S*>(out), static_cast<const S*>(in0),
+            static_cast<const S*>(in1), n, f);
+    } else {
+        flat_kernel<T, NIN, F><<<flat_grid(npackets), kBlock, 0, stream(device)>>>(
+            static_cast<const S*>(in0), static_cast<const S*>(in1), static_cast<S*>(out),
+            npackets, n, f);
+    }
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+int mode_of(const int64_t* strides, int64_t C, bool two_d) {
+    const int64_t sr = two_d ? strides[0] : 0;
+    const int64_t sc = two_d ? strides[1] : strides[0];
+    if (sc == 1 && (!two_d || sr == C)) return kFull;
+    if (sc == 1 && sr == 0) return kRowB;
+    if (sc == 0 && sr == 1 && two_d) return kColB;
+    if (sc == 0 && sr == 0) return kScal;
+    return -1;
+}
+
+template <typename T, int MA, int MB, typename F>
+void launch_binary2d(int device, const void* a, const void* b, void* out, int64_t n, int64_t C,
+                     F f) {
+    using S = typename Elem<T>::storage;
+    constexpr int N = Packet<T>::N;
+    const int64_t npackets = n / N;
+    const bool big = n >= (int64_t(1) << 31);
+    const FastDiv cdiv = make_fastdiv(static_cast<uint32_t>(big ? 1 : C));
+    if (big) {
+        binary2d_kernel<T, MA, MB, true, F><<<flat_grid(npackets), kBlock, 0, stream(device)>>>(
+            static_cast<const S*>(a), static_cast<const S*>(b), static_cast<S*>(out), npackets,
+            C, cdiv, f);
+    } else {
+        binary2d_kernel<T, MA, MB, false, F><<<flat_grid(npackets), kBlock, 0, stream(device)>>>(
+            static_cast<const S*>(a), static_cast<const S*>(b), static_cast<S*>(out), npackets,
+            C, cdiv, f);
+    }
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+// Mode pairs with a specialised kernel; other combinations take nd_kernel.
+template <typename T, typename F>
+bool try_binary2d(int device, int ma, int mb, const void* a, const void* b, void* out,
+                  int64_t n, int64_t C, F f) {
+#define TP_AMD_PAIR(MA, MB)                                                       \
+    if (ma == MA && mb == MB) {                                                   \
+        launch_binary2d<T, MA, MB, F>(device, a, b, out, n, C, f);                \
+        return true;                                                              \
+    }
+    TP_AMD_PAIR(kFull, kFull)
+    TP_AMD_PAIR(kFull, kRowB)
+    TP_AMD_PAIR(kFull, kColB)
+    TP_AMD_PAIR(kFull, kScal)
+    TP_AMD_PAIR(kRowB, kFull)
+    TP_AMD_PAIR(kColB, kFull)
+    TP_AMD_PAIR(kScal, kFull)
+    TP_AMD_PAIR(kColB, kRowB)
+    TP_AMD_PAIR(kRowB, kColB)
+#undef TP_AMD_PAIR
+    return false;
+}
+
+template <typename T, typename F>
+void binary_typed(int device, int ndim, const int64_t* sizes, const void* a,
+                  const int64_t* as, const void* b, const int64_t* bs, void* out,
+                  const int64_t* os, F f) {
+    using S = typename Elem<T>::storage;
+    constexpr int N = Packet<T>::N;
+    const int64_t* strides[3] = {os, as, bs};
+    const Layout<3> l = coalesce<3>(ndim, sizes, strides);
+    const int64_t n = l.numel();
+    if (n == 0) return;
+    if (l.ndim <= 2) {
+        const bool two_d = l.ndim == 2;
+        const int64_t C = l.ndim == 0 ? 1 : l.sizes[l.ndim - 1];
+        int64_t zero[2] = {0, 0};
+        const int64_t* so = l.ndim == 0 ? zero : l.strides[0];
+        const int64_t* sa = l.ndim == 0 ? zero : l.strides[1];
+        const int64_t* sb = l.ndim == 0 ? zero : l.strides[2];
+        const int mo = l.ndim == 0 ? kFull : mode_of(so, C, two_d);
+        const int ma = l.ndim == 0 ? kFull : mode_of(sa, C, two_d);
+        const int mb = l.ndim == 0 ? kFull : mode_of(sb, C, two_d);
+        const bool packets = C % N == 0 && aligned16(out) &&
+                             (ma == kColB || ma == kScal || aligned16(a)) &&
+                             (mb == kColB || mb == kScal || aligned16(b));
+        if (mo == kFull && ma >= 0 && mb >= 0 && packets &&
+            try_binary2d<T>(device, ma, mb, a, b, out, n, C, f)) {
+            return;
+        }
+    }
+    nd_kernel<T, 2, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
+        nd_params(l), static_cast<S*>(out), static_cast<const S*>(a), static_cast<const S*>(b),
+        n, f);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+template <typename T, typename F>
+void unary_typed(int device, int ndim, const int64_t* sizes, const void* x, const int64_t* xs,
+                 void* y, F f) {
+    using S = typename Elem<T>::storage;
+    int64_t ys[TP_AMD_MAX_DIMS];
+    contiguous_strides(ndim, sizes, ys);
+    const int64_t* strides[2] = {ys, xs};
+    const Layout<2> l = coalesce<2>(ndim, sizes, strides);
+    const int64_t n = l.numel();
+    if (n == 0) return;
+    if (l.ndim == 0 || (l.ndim == 1 && l.strides[0][0] == 1 && l.strides[1][0] == 1)) {
+        launch_flat<T, 1, F>(device, x, nullptr, y, n, f);
+        return;
+    }
+    nd_kernel<T, 1, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
+        nd_params(l), static_cast<S*>(y), static_cast<const S*>(x), nullptr, n, f);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+#define TP_AMD_UNARY_CASE(OP)                                                         \
+    case OP:                                                                          \
+        unary_typed<T>(index, ndim, sizes, x, x_strides, y, UnaryFn<OP>{param});      \
+        break;
+
+template <typename T>
+void unary_dispatch(int index, int op, int ndim, const int64_t* sizes, const void* x,
+                    const int64_t* x_strides, void* y, float param) {
+    switch (op) {
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_EXP)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_LOG)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_SQRT)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_RSQRT)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_NEG)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_ABS)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_SQUARE)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_POW)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_RELU)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_SIGMOID)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_TANH)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_SILU)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_GELU)
+        TP_AMD_UNARY_CASE(TP_AMD_UNARY_GELU_TANH)
+        default: TP_AMD_CHECK(false, "unknown unary op ", op);
+    }
+}
+#undef TP_AMD_UNARY_CASE
+
+#define TP_AMD_BWD_CASE(OP)                                                            \
+    case OP:                                                                           \
+        launch_flat<T, 2>(index, grad, saved, dx, n, BackwardFn<OP>{param});           \
+        break;
+
+template <typename T>
+void backward_dispatch(int index, int op, int64_t n, const void* grad, const void* saved,
+                       void* dx, float param) {
+    switch (op) {
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_THRESHOLD)
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_SIGMOID)
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_TANH)
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_GELU)
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_GELU_TANH)
+        TP_AMD_BWD_CASE(TP_AMD_BACKWARD_SILU)
+        default: TP_AMD_CHECK(false, "unknown backward op ", op);
+    }
+}
+#undef TP_AMD_BWD_CASE
+
+}  // namespace
+
+}  // namespace tp_amd
+
+using namespace tp_amd;
+
+extern "C" {
+
+int tp_amd_launch_binary(int device, int op, int dtype, int ndim, const int64_t* sizes,
+                         const void* a, const int64_t* a_strides, const void* b,
+                         const int64_t* b_strides, void* out, const int64_t* out_strides,
+                         float alpha) {
+    return guarded([&] {
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        TP_AMD_DISPATCH_FLOAT(dtype, T, {
+            switch (op) {
+                case TP_AMD_BINARY_ADD:
+                    binary_typed<T>(index, ndim, sizes, a, a_strides, b, b_strides, out,
+                                    out_strides, BinaryFn<TP_AMD_BINARY_ADD>{alpha});
+                    break;
+                case TP_AMD_BINARY_MUL:
+                    binary_typed<T>(index, ndim, sizes, a, a_strides, b, b_strides, out,
+                                    out_strides, BinaryFn<TP_AMD_BINARY_MUL>{alpha});
+                    break;
+                case TP_AMD_BINARY_DIV:
+                    binary_typed<T>(index, ndim, sizes, a, a_strides, b, b_strides, out,
+                                    out_strides, BinaryFn<TP_AMD_BINARY_DIV>{alpha});
+                    break;
+                default: TP_AMD_CHECK(false, "unknown binary op ", op);
+            }
+        });
+    });
+}
+
+int tp_amd_launch_affine(int device, int dtype, int64_t n, const void* x, float alpha,
+                         float beta, void* y) {
+    return guarded([&] {
+        TP_AMD_CHECK(n >= 0, "negative element count");
+        if (n == 0) return;
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        TP_AMD_DISPATCH_FLOAT(dtype, T,
+                              launch_flat<T, 1>(index, x, nullptr, y, n, AffineFn{alpha, beta}));
+    });
+}
+
+int tp_amd_launch_unary(int device, int op, int dtype, int ndim, const int64_t* sizes,
+                        const void* x, const int64_t* x_strides, void* y, float param) {
+    return guarded([&] {
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        TP_AMD_DISPATCH_FLOAT(dtype, T,
+                              unary_dispatch<T>(index, op, ndim, sizes, x, x_strides, y, param));
+    });
+}
+
+int tp_amd_launch_activation_backward(int device, int op, int dtype, int64_t n,
+                                      const void* grad, const void* saved, void* dx,
+                                      float param) {
+    return guarded([&] {
+        TP_AMD_CHECK(n >= 0, "negative element count");
+        if (n == 0) return;
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        TP_AMD_DISPATCH_FLOAT(dtype, T,
+                              backward_dispatch<T>(index, op, n, grad, saved, dx, param));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,32 @@
+// Shared argument block and launch entry of the GEMM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tp_amd {
+
+struct GemmArgs {
+    int64_t batch, m, n, k;
+    float alpha, beta;
+    const void* a;
+    int64_t lda, stride_a;
+    const void* b;
+    int64_t ldb, stride_b;
+    const void* cin;
+    int64_t cin_rs, cin_cs, cin_stride_b;
+    void* c;
+    int64_t ldc, stride_c;
+    bool trans_a, trans_b;
+};
+
+// Any shape, stride and alignment (gemm.hip).
+template <typename T>
+void launch_gemm_general(const GemmArgs& p, hipStream_t stream);
+
+// Picks the matrix-core kernel when the operands allow it, the general one
+// otherwise (gemm_mfma.hip).
+void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream);
+
+}  // namespace tp_amd

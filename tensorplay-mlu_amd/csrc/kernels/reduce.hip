@@ -1,0 +1,381 @@
+// Reductions for gfx950: sum, mean, amax, amin of a dense [outer, r, inner]
+// array along the middle axis (the reference's cnnlReduce_v2,
+// tensorplay_mlu/csrc/ReduceKernels.cpp:21-44).
+//
+// * inner == 1 (row reductions): a wavefront (or, for long rows, a whole
+//   256-thread block) reduces one row segment with 16-byte packet loads,
+//   then combines across lanes with DPP/shuffle steps and across waves in
+//   LDS.  When there are too few rows to fill 256 CUs, rows are split into
+//   segments whose float32 partials a second pass combines.
+// * inner > 1 (column reductions, e.g. dim 0 of [32768, 4096]): lanes walk
+//   the contiguous inner axis with packets, four row groups per block share
+//   the rows of a chunk, and chunks of rows are spread over the grid; a
+//   second pass combines the chunk partials.
+// Arithmetic is float32.  amax/amin skip NaN inputs and order -0 below +0,
+// so every evaluation order gives the same bits.
+
+#include <cmath>
+
+#include "device_common.h"
+#include "../allocator.h"
+#include "../runtime.h"
+#include "tp_amd_kernels.h"
+
+namespace tp_amd {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int OP>
+struct Combine;
+
+template <>
+struct Combine<TP_AMD_REDUCE_SUM> {
+    __device__ __forceinline__ static float identity() { return 0.0f; }
+    __device__ __forceinline__ static float apply(float a, float b) { return a + b; }
+};
+template <>
+struct Combine<TP_AMD_REDUCE_MEAN> : Combine<TP_AMD_REDUCE_SUM> {};
+template <>
+struct Combine<TP_AMD_REDUCE_AMAX> {
+    __device__ __forceinline__ static float identity() { return __uint_as_float(0x7fc00000u); }
+    __device__ __forceinline__ static float apply(float a, float b) {
+        if (a != a) return b;
+        if (b != b) return a;
+        if (a == b) return (__float_as_uint(a) & 0x80000000u) ? b : a;  // +0 over -0
+        return a > b ? a : b;
+    }
+};
+template <>
+struct Combine<TP_AMD_REDUCE_AMIN> {
+    __device__ __forceinline__ static float identity() { return __uint_as_float(0x7fc00000u); }
+    __device__ __forceinline__ static float apply(float a, float b) {
+        if (a != a) return b;
+        if (b != b) return a;
+        if (a == b) return (__float_as_uint(a) & 0x80000000u) ? a : b;  // -0 over +0
+        return a < b ? a : b;
+    }
+};
+
+template <int OP>
+__device__ __forceinline__ float wave_reduce(float v) {
+#pragma unroll
+    for (int mask = kWave / 2; mask > 0; mask >>= 1) {
+        v = Combine<OP>::apply(v, wave_shfl_xor(v, mask));
+    }
+    return v;
+}
+
+// Final value of a reduction: the mean divides the float32 sum by the
+// number of reduced elements.
+template <int OP>
+__device__ __forceinline__ float finish(float v, int64_t count, bool final_pass) {
+    if constexpr (OP == TP_AMD_REDUCE_MEAN) {
+        if (final_pass) return v / static_cast<float>(count);
+    }
+    return v;
+}
+
+// Row segments.  Segment s covers row s / nseg, elements
+// [(s % nseg) * chunk, min(r, ... + chunk)).  WAVES wavefronts share one
+// segment (1: each wave of the block takes its own segment).
+template <typename Tin, typename Tout, int OP, int WAVES, bool VEC>
+__global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
+    const typename Elem<Tin>::storage* x, typename Elem<Tout>::storage* out, int64_t nsegs,
+    int64_t r, int64_t chunk, int64_t nseg, bool final_pass, int64_t count) {
+    constexpr int N = VEC ? Packet<Tin>::N : 1;
+    constexpr int kSegsPerBlock = (kBlock / kWave) / WAVES;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int64_t seg = static_cast<int64_t>(blockIdx.x) * kSegsPerBlock + wave / WAVES;
+    const int tid = (wave % WAVES) * kWave + lane;  // thread index within the segment
+    constexpr int kThreads = WAVES * kWave;
+    float acc = Combine<OP>::identity();
+    if (seg < nsegs) {
+        const int64_t row = seg / nseg, part = seg - row * nseg;
+        const int64_t begin = part * chunk;
+        const int64_t end = begin + chunk < r ? begin + chunk : r;
+        const typename Elem<Tin>::storage* p = x + row * r;
+        if constexpr (VEC) {
+            // begin and end are multiples of N (chunk and r are).
+            const int64_t pb = begin / N, pe = end / N;
+            constexpr int U = 4;
+            int64_t q = pb + tid;
+            for (; q + (U - 1) * kThreads < pe; q += U * kThreads) {
+                Packet<Tin> v[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = load_packet_nt<Tin>(p + (q + u * kThreads) * N);
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        acc = Combine<OP>::apply(acc, Elem<Tin>::load(v[u].v[j]));
+            }
+            for (; q < pe; q += kThreads) {
+                const Packet<Tin> v = load_packet_nt<Tin>(p + q * N);
+#pragma unroll
+                for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v.v[j]));
+            }
+        } else {
+            for (int64_t j = begin + tid; j < end; j += kThreads) {
+                acc = Combine<OP>::apply(acc, Elem<Tin>::load(p[j]));
+            }
+        }
+    }
+    acc = wave_reduce<OP>(acc);
+    if constexpr (WAVES > 1) {
+        __shared__ float partial[kBlock / kWave];
+        if (lane == 0) partial[wave] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            acc = lane < WAVES ? partial[lane] : Combine<OP>::identity();
+            acc = wave_reduce<OP>(acc);
+        }
+        if (threadIdx.x == 0 && seg < nsegs) {
+            out[seg] = Elem<Tout>::store(finish<OP>(acc, count, final_pass));
+        }
+    } else {
+        if (lane == 0 && seg < nsegs) out[seg] = Elem<Tout>::store(finish<OP>(acc, count, final_pass));
+    }
+}
+
+// Column chunks.  Block (bx, ch, z): columns [bx * 64 * N, +64 * N) of every
+// outer index o = z, z + gridDim.z, ...; rows [ch * chunk, +chunk) split
+// over 4 row groups.  Writes out[(o * nchunk + ch) * inner + col].
+constexpr int kColLanes = 64;
+constexpr int kRowGroups = kBlock / kColLanes;
+
+template <typename Tin, typename Tout, int OP, bool VEC>
+__global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
+    const typename Elem<Tin>::storage* x, typename Elem<Tout>::storage* out, int64_t outer,
+    int64_t r, int64_t inner, int64_t chunk, int64_t nchunk, bool final_pass, int64_t count) {
+    constexpr int N = VEC ? Packet<Tin>::N : 1;
+    __shared__ float partial[kRowGroups][kColLanes * N + 1];
+    const int lane = threadIdx.x % kColLanes, rg = threadIdx.x / kColLanes;
+    const int64_t col = (static_cast<int64_t>(blockIdx.x) * kColLanes + lane) * N;
+    const int64_t ch = blockIdx.y;
+    const int64_t begin = ch * chunk;
+    const int64_t end = begin + chunk < r ? begin + chunk : r;
+    for (int64_t o = blockIdx.z; o < outer; o += gridDim.z) {
+        float acc[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[j] = Combine<OP>::identity();
+        if (col < inner) {
+            const typename Elem<Tin>::storage* p = x + o * r * inner + col;
+            int64_t row = begin + rg;
+            constexpr int U = 4;
+            for (; row + (U - 1) * kRowGroups < end; row += U * kRowGroups) {
+                if constexpr (VEC) {
+                    Packet<Tin> v[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u)
+                        v[u] = load_packet_nt<Tin>(p + (row + u * kRowGroups) * inner);
+#pragma unroll
+                    for (int u = 0; u < U; ++u)
+#pragma unroll
+                        for (int j = 0; j < N; ++j)
+                            acc[j] = Combine<OP>::apply(acc[j], Elem<Tin>::load(v[u].v[j]));
+                } else {
+                    typename Elem<Tin>::storage v[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) v[u] = p[(row + u * kRowGroups) * inner];
+#pragma unroll
+                    for (int u = 0; u < U; ++u)
+                        acc[0] = Combine<OP>::apply(acc[0], Elem<Tin>::load(v[u]));
+                }
+            }
+            for (; row < end; row += kRowGroups) {
+                if constexpr (VEC) {
+                    const Packet<Tin> v = load_packet_nt<Tin>(p + row * inner);
+#pragma unroll
+                    for (int j = 0; j < N; ++j)
+                        acc[j] = Combine<OP>::apply(acc[j], Elem<Tin>::load(v.v[j]));
+                } else {
+                    acc[0] = Combine<OP>::apply(acc[0], Elem<Tin>::load(p[row * inner]));
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) partial[rg][lane * N + j] = acc[j];
+        __syncthreads();
+        // Row group 0 combines the four groups in a fixed order.
+        for (int e = threadIdx.x; e < kColLanes * N; e += kBlock) {
+            float v = partial[0][e];
+#pragma unroll
+            for (int g = 1; g < kRowGroups; ++g) v = Combine<OP>::apply(v, partial[g][e]);
+            const int64_t c = static_cast<int64_t>(blockIdx.x) * kColLanes * N + e;
+            if (c < inner) {
+                out[(o * nchunk + ch) * inner + c] =
+                    Elem<Tout>::store(finish<OP>(v, count, final_pass));
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T, int OP>
+void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const void* xv,
+                  void* outv) {
+    using S = typename Elem<T>::storage;
+    const S* x = static_cast<const S*>(xv);
+    S* out = static_cast<S*>(outv);
+    hipStream_t st = stream(device);
+    const int64_t cus = cu_count(device);
+    constexpr int N = Packet<T>::N;
+    if (inner == 1) {
+        const bool vec = r % N == 0 && aligned16(x);
+        // Enough independent rows fill the chip; otherwise split the rows.
+        const int64_t target_segs = cus * 16;
+        int64_t nseg = 1;
+        if (outer < target_segs && r >= 8192) {
+            nseg = (target_segs + outer - 1) / outer;
+            const int64_t max_seg = r / 2048;  // keep segments >= 2048 elements
+            if (nseg > max_seg) nseg = max_seg > 1 ? max_seg : 1;
+        }
+        int64_t chunk = (r + nseg - 1) / nseg;
+        if (vec) chunk = (chunk + N - 1) / N * N;
+        nseg = (r + chunk - 1) / chunk;
+        const int64_t nsegs = outer * nseg;
+        const bool long_rows = chunk >= 4096;
+        auto launch_rows = [&](auto waves_tag, auto vec_tag, auto* dst, bool final_pass) {
+            constexpr int W = decltype(waves_tag)::value;
+            constexpr bool V = decltype(vec_tag)::value;
+            using Tout = std::remove_pointer_t<decltype(dst)>;
+            constexpr int per_block = (kBlock / kWave) / W;
+            const int64_t blocks = (nsegs + per_block - 1) / per_block;
+            using TO = std::conditional_t<std::is_same<Tout, float>::value, float, T>;
+            reduce_rows_kernel<T, TO, OP, W, V><<<blocks, kBlock, 0, st>>>(
+                x, reinterpret_cast<typename Elem<TO>::storage*>(dst), nsegs, r, chunk, nseg,
+                final_pass, r);
+        };
+        using One = std::integral_constant<int, 1>;
+        using Four = std::integral_constant<int, 4>;
+        using Yes = std::true_type;
+        using No = std::false_type;
+        if (nseg == 1) {
+            if (long_rows) {
+                vec ? launch_rows(Four{}, Yes{}, out, true) : launch_rows(Four{}, No{}, out, true);
+            } else {
+                vec ? launch_rows(One{}, Yes{}, out, true) : launch_rows(One{}, No{}, out, true);
+            }
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            return;
+        }
+        Workspace ws(static_cast<size_t>(nsegs) * sizeof(float), device);
+        float* partial = static_cast<float*>(ws.get());
+        if (long_rows) {
+            vec ? launch_rows(Four{}, Yes{}, partial, false)
+                : launch_rows(Four{}, No{}, partial, false);
+        } else {
+            vec ? launch_rows(One{}, Yes{}, partial, false)
+                : launch_rows(One{}, No{}, partial, false);
+        }
+        TP_AMD_HIP_CHECK(hipGetLastError());
+        // Second pass: one wave per row over its nseg float32 partials.
+        const int64_t blocks = (outer + (kBlock / kWave) - 1) / (kBlock / kWave);
+        reduce_rows_kernel<float, T, OP, 1, false><<<blocks, kBlock, 0, st>>>(
+            partial, out, outer, nseg, nseg, 1, true, r);
+        TP_AMD_HIP_CHECK(hipGetLastError());
+        return;
+    }
+    // Column reductions.
+    const bool vec = inner % N == 0 && aligned16(x);
+    const int64_t cols_per_block = static_cast<int64_t>(kColLanes) * (vec ? N : 1);
+    const int64_t bx = (inner + cols_per_block - 1) / cols_per_block;
+    const int64_t z = outer < 65535 ? outer : 65535;
+    const int64_t base_blocks = bx * z;
+    const int64_t target_blocks = cus * 8;
+    int64_t nchunk = 1;
+    if (base_blocks < target_blocks && r >= 64) {
+        nchunk = (target_blocks + base_blocks - 1) / base_blocks;
+        const int64_t max_chunks = r / 32;  // keep >= 32 rows per chunk
+        if (nchunk > max_chunks) nchunk = max_chunks > 1 ? max_chunks : 1;
+        if (nchunk > 65535) nchunk = 65535;
+    }
+    const int64_t chunk = (r + nchunk - 1) / nchunk;
+    nchunk = (r + chunk - 1) / chunk;
+    const dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(nchunk),
+                    static_cast<unsigned>(z));
+    if (nchunk == 1) {
+        if (vec) {
+            reduce_cols_kernel<T, T, OP, true><<<grid, kBlock, 0, st>>>(x, out, outer, r, inner,
+                                                                       chunk, 1, true, r);
+        } else {
+            reduce_cols_kernel<T, T, OP, false><<<grid, kBlock, 0, st>>>(x, out, outer, r, inner,
+                                                                        chunk, 1, true, r);
+        }
+        TP_AMD_HIP_CHECK(hipGetLastError());
+        return;
+    }
+    Workspace ws(static_cast<size_t>(outer) * nchunk * inner * sizeof(float), device);
+    float* partial = static_cast<float*>(ws.get());
+    if (vec) {
+        reduce_cols_kernel<T, float, OP, true><<<grid, kBlock, 0, st>>>(
+            x, partial, outer, r, inner, chunk, nchunk, false, r);
+    } else {
+        reduce_cols_kernel<T, float, OP, false><<<grid, kBlock, 0, st>>>(
+            x, partial, outer, r, inner, chunk, nchunk, false, r);
+    }
+    TP_AMD_HIP_CHECK(hipGetLastError());
+    const bool vec2 = inner % 4 == 0;
+    const int64_t cpb2 = static_cast<int64_t>(kColLanes) * (vec2 ? 4 : 1);
+    const dim3 grid2(static_cast<unsigned>((inner + cpb2 - 1) / cpb2), 1u,
+                     static_cast<unsigned>(z));
+    if (vec2) {
+        reduce_cols_kernel<float, T, OP, true><<<grid2, kBlock, 0, st>>>(
+            partial, out, outer, nchunk, inner, nchunk, 1, true, r);
+    } else {
+        reduce_cols_kernel<float, T, OP, false><<<grid2, kBlock, 0, st>>>(
+            partial, out, outer, nchunk, inner, nchunk, 1, true, r);
+    }
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+template <typename T>
+void reduce_dispatch_op(int device, int op, int64_t outer, int64_t r, int64_t inner,
+                        const void* x, void* out) {
+    switch (op) {
+        case TP_AMD_REDUCE_SUM:
+            reduce_typed<T, TP_AMD_REDUCE_SUM>(device, outer, r, inner, x, out);
+            break;
+        case TP_AMD_REDUCE_MEAN:
+            reduce_typed<T, TP_AMD_REDUCE_MEAN>(device, outer, r, inner, x, out);
+            break;
+        case TP_AMD_REDUCE_AMAX:
+            reduce_typed<T, TP_AMD_REDUCE_AMAX>(device, outer, r, inner, x, out);
+            break;
+        case TP_AMD_REDUCE_AMIN:
+            reduce_typed<T, TP_AMD_REDUCE_AMIN>(device, outer, r, inner, x, out);
+            break;
+        default: TP_AMD_CHECK(false, "unknown reduce op ", op);
+    }
+}
+
+}  // namespace
+
+}  // namespace tp_amd
+
+using namespace tp_amd;
+
+extern "C" {
+
+int tp_amd_launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r,
+                         int64_t inner, const void* x, void* out) {
+    return guarded([&] {
+        TP_AMD_CHECK(outer >= 0 && r >= 0 && inner >= 0, "negative reduce extent");
+        if (outer == 0 || inner == 0) return;
+        TP_AMD_CHECK(r > 0, "reduce over an empty axis: the caller fills the result");
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        switch (dtype) {
+            case TP_AMD_FLOAT32: reduce_dispatch_op<float>(index, op, outer, r, inner, x, out); break;
+            case TP_AMD_BFLOAT16: reduce_dispatch_op<bf16_t>(index, op, outer, r, inner, x, out); break;
+            case TP_AMD_FLOAT16: reduce_dispatch_op<f16_t>(index, op, outer, r, inner, x, out); break;
+            default:
+                TP_AMD_CHECK(false, "reductions take float32, float16 or bfloat16, got ",
+                             dtype_name(dtype));
+        }
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+"""Copies, casts, fills and factories on the GPU (the reference's cases,
+tests/test_mlu.py:64-132): every result bit-exact against the host data or
+the CPU oracle's conversion."""
+
+import importlib
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32, assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+F64, I8, I16, I32, I64, U8, BOOL = 3, 4, 5, 6, 7, 8, 9
+ALL = [F32, F16, BF16, F64, I8, I16, I32, I64, U8, BOOL]
+NP = {F32: np.float32, F16: np.float16, BF16: np.uint16, F64: np.float64, I8: np.int8,
+      I16: np.int16, I32: np.int32, I64: np.int64, U8: np.uint8, BOOL: np.bool_}
+
+
+def values(orc, shape, dtype, seed=0):
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * 10
+    if dtype in (F32, F16, BF16):
+        return orc.from_float(x, dtype)
+    return orc.cast(F32, dtype, x)
+
+
+@pytest.mark.parametrize("dtype", ALL)
+def test_round_trip(dev, orc, dtype):
+    x = values(orc, (5, 7), dtype)
+    d = dev.from_numpy(x, dtype=dtype)
+    assert d.dtype == dtype and d.shape == (5, 7)
+    assert_bitexact(d.numpy(), x, "round trip")
+
+
+def test_strided_copies_both_ways(dev, ops, orc):
+    x = values(orc, (6, 8), F32)
+    # host strided source -> device
+    d = dev.empty((8, 6), F32)
+    ops.copy_(d, x.T)
+    assert_bitexact(d.numpy(), np.ascontiguousarray(x.T), "host .T -> device")
+    d = dev.from_numpy(x)
+    assert_bitexact(d.t().numpy(), np.ascontiguousarray(x.T), "device .t() -> host")
+    assert_bitexact(d[:, 1::3].numpy(), np.ascontiguousarray(x[:, 1::3]), "device slice -> host")
+    out = ops.zeros_like(d.t())
+    ops.copy_(out, d.t())
+    assert_bitexact(out.numpy(), np.ascontiguousarray(x.T), "device .t() -> device")
+    # a large transpose (LDS-tiled kernel) and a strided destination
+    big = values(orc, (1000, 777), F32, 1)
+    db = dev.from_numpy(big)
+    assert_bitexact(ops.contiguous(db.t()).numpy(), np.ascontiguousarray(big.T), "transpose")
+    dst = dev.from_numpy(np.zeros((777, 1000), np.float32))
+    ops.copy_(dst.t(), db)
+    assert_bitexact(dst.numpy(), np.ascontiguousarray(big.T), "into transposed view")
+
+
+def test_broadcasting_copy_on_device(dev, ops, orc):
+    row = values(orc, (1, 5), F32)
+    out = dev.empty((4, 5), F32)
+    ops.copy_(out, dev.from_numpy(row))
+    assert_bitexact(out.numpy(), np.broadcast_to(row, (4, 5)).copy(), "broadcast copy")
+
+
+@pytest.mark.parametrize("src,dst", [(F32, F16), (F16, F32), (F32, BF16), (BF16, F32),
+                                     (F16, BF16), (F32, I32), (I64, F32), (F64, F32),
+                                     (F32, F64), (F64, BF16), (I32, I8), (BOOL, F32),
+                                     (F32, BOOL), (U8, I64), (BF16, I64)])
+def test_casts_on_device(dev, ops, orc, src, dst):
+    x = values(orc, (3, 9), src)
+    got = ops.to(dev.from_numpy(x, dtype=src), dst).numpy()
+    want = orc.cast(src, dst, x) if not (src == F16 and dst == BF16) else \
+        orc.cast(F32, BF16, orc.cast(F16, F32, x))
+    assert_bitexact(got, want, f"cast {src}->{dst}")
+
+
+def test_cast_every_bf16_and_f16_pattern(dev, ops, orc):
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    for dtype in (BF16, F16):
+        d = dev.from_numpy(bits, dtype=dtype)
+        got = ops.to(d, F32).numpy()
+        want = orc.cast(dtype, F32, bits)
+        nan = np.isnan(want)
+        assert_bitexact(got[~nan], want[~nan], f"{dtype} -> f32")
+        assert np.isnan(got[nan]).all()
+    f = np.random.default_rng(0).standard_normal(1 << 20).astype(np.float32) * 1e3
+    f[:6] = [np.inf, -np.inf, 0.0, -0.0, 3.4e38, 1e-40]
+    for dtype in (BF16, F16):
+        got = ops.to(dev.from_numpy(f), dtype).numpy()
+        assert_bitexact(got, orc.cast(F32, dtype, f), f"f32 -> {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ALL)
+def test_fill_and_factories(dev, ops, dtype):
+    d = dev.empty((3, 4), dtype)
+    value = 2.5 if dtype in (F32, F16, BF16, F64) else 3
+    ops.fill_(d, value)
+    want_val = {F16: np.float16(2.5).view(np.uint16), BF16: np.uint16(0x4020)}.get(dtype, value)
+    assert_bitexact(d.numpy(), np.full((3, 4), want_val, dtype=NP[dtype]), "fill_")
+    ops.zero_(d)
+    assert_bitexact(d.numpy(), np.zeros((3, 4), NP[dtype]), "zero_")
+    one = {F16: np.float16(1).view(np.uint16), BF16: np.uint16(0x3f80)}.get(dtype, 1)
+    assert_bitexact(ops.ones_like(d).numpy(), np.full((3, 4), one, NP[dtype]), "ones_like")
+    assert_bitexact(ops.zeros_like(d).numpy(), np.zeros((3, 4), NP[dtype]), "zeros_like")
+    assert ops.ones_like(d, dtype=F32).dtype == F32
+    seven = {F16: np.float16(7).view(np.uint16), BF16: np.uint16(0x40e0)}.get(dtype, 7)
+    assert_bitexact(ops.full_like(d, 7).numpy(), np.full((3, 4), seven, NP[dtype]), "full_like")
+    big = dev.empty((1000, 333), dtype)
+    ops.fill_(big, value)
+    assert_bitexact(big.numpy(), np.full((1000, 333), want_val, dtype=NP[dtype]), "large fill")
+
+
+def test_views_share_device_memory(dev, ops, orc):
+    x = values(orc, (4, 6), F32)
+    d = dev.from_numpy(x)
+    v = d.view(6, 4)
+    ops.mul__scalar(v, 2.0)
+    assert_bitexact(d.numpy(), x * np.float32(2), "view mul_")
+    assert_bitexact(ops.contiguous(d.permute(1, 0)).numpy().reshape(-1),
+                    (x * np.float32(2)).T.reshape(-1), "permute")
+    assert_bitexact(d[1:3].numpy(), (x * np.float32(2))[1:3], "narrow")
+
+
+def test_item_clone_and_empty(dev, ops, orc):
+    x = values(orc, (1,), F32)
+    assert ops.item(dev.from_numpy(x)) == float(x[0])
+    assert ops.item(dev.from_numpy(np.array([7], np.int64))) == 7
+    c = ops.clone(dev.from_numpy(x))
+    assert_bitexact(c.numpy(), x, "clone")
+    e = ops.empty((0, 3))
+    assert e.shape == (0, 3) and e.numel() == 0
+    tensor = importlib.import_module("tensorplay-mlu_amd.tensor")
+    with pytest.raises(tensor.DeviceError):
+        ops.item(dev.from_numpy(values(orc, (2,), F32)))
+
+
+def test_memory_statistics(dev, ops):
+    runtime = importlib.import_module("tensorplay-mlu_amd.runtime")
+    runtime.synchronize()
+    runtime.empty_cache()
+    before = runtime.memory_allocated()
+    x = ops.empty((1 << 20,))
+    assert runtime.memory_allocated() >= before + (4 << 20)
+    assert runtime.max_memory_allocated() >= runtime.memory_allocated()
+    del x
+    assert runtime.memory_allocated() == before
+    assert runtime.memory_reserved() >= before
+    free, total = runtime.mem_get_info()
+    assert 0 < free <= total
+    assert runtime.device_count() >= 1 and runtime.current_device() == 0

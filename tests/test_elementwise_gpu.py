@@ -1,0 +1,255 @@
+"""Elementwise operators on the GPU against the CPU oracle (same seeded
+inputs): binary arithmetic with broadcasting, in-place and scalar forms,
+unary math, activations and their backward kernels.
+
+Mirrors the reference's cases (tests/test_mlu.py:137-233) and runs config 2
+of the benchmark at full size ([8192, 8192] with row and column
+broadcasts).  Tolerances are stated in tests/_check.py.
+"""
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32, assert_bitexact, assert_elementwise
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [F32, BF16, F16]
+ADD, MUL, DIV = 0, 1, 2
+
+
+def sample(orc, shape, dtype, seed=0, low=None, high=None):
+    g = np.random.default_rng(seed)
+    if low is None:
+        x = g.standard_normal(shape, dtype=np.float32)
+    else:
+        x = g.uniform(low, high, size=shape).astype(np.float32)
+    return orc.from_float(x, dtype)
+
+
+def up(dev, arr, dtype):
+    return dev.from_numpy(arr, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("sa,sb", [((4, 1, 5), (3, 1)), ((6, 4), (4,)), ((33, 17), (33, 1)),
+                                   ((64, 128), (64, 128)), ((5, 7), ()), ((1, 9), (8, 1))])
+def test_binary_with_broadcasting(dev, ops, orc, dtype, sa, sb):
+    a = sample(orc, sa, dtype, 0)
+    b = sample(orc, sb, dtype, 1, 0.5, 2.0)
+    da, db = up(dev, a, dtype), up(dev, b, dtype)
+    assert_bitexact(ops.add(da, db).numpy(), orc.binary(ADD, dtype, a, b, 1.0), "add")
+    assert_bitexact(ops.sub(da, db).numpy(), orc.binary(ADD, dtype, a, b, -1.0), "sub")
+    assert_elementwise(ops.sub(da, db, alpha=2).numpy(), orc.binary(ADD, dtype, a, b, -2.0),
+                       dtype, "sub alpha=2", max_ulp=1)
+    assert_elementwise(ops.add(da, db, alpha=0.5).numpy(), orc.binary(ADD, dtype, a, b, 0.5),
+                       dtype, "add alpha=0.5", max_ulp=1)
+    assert_bitexact(ops.mul(da, db).numpy(), orc.binary(MUL, dtype, a, b), "mul")
+    assert_bitexact(ops.div(da, db).numpy(), orc.binary(DIV, dtype, a, b), "div")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_scalar_forms_and_host_scalars(dev, ops, orc, dtype):
+    a = sample(orc, (8, 3), dtype)
+    d = up(dev, a, dtype)
+    cases = [
+        (ops.add_scalar(d, 2), orc.affine(dtype, a, 1.0, 2.0)),
+        (ops.mul_scalar(d, 3), orc.affine(dtype, a, 3.0, 0.0)),
+        # division multiplies by the float32 reciprocal (BinaryKernels.cpp:231)
+        (ops.div_scalar(d, 3), orc.affine(dtype, a, np.float32(1.0 / 3.0), 0.0)),
+        (ops.rsub_scalar(d, 1), orc.affine(dtype, a, -1.0, 1.0)),
+        (ops.sub_scalar(d, 2, alpha=3), orc.affine(dtype, a, 1.0, -6.0)),
+        (ops.mul(d, np.float32(2.0)), orc.affine(dtype, a, 2.0, 0.0)),
+        (ops.add(np.float32(2.0), d), orc.affine(dtype, a, 1.0, 2.0)),
+        (ops.sub(np.float32(2.0), d), orc.affine(dtype, a, -1.0, 2.0)),
+        (ops.div(d, np.float32(4.0)), orc.affine(dtype, a, 0.25, 0.0)),
+    ]
+    for i, (got, want) in enumerate(cases):
+        assert_elementwise(got.numpy(), want, dtype, f"case {i}", max_ulp=1)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_in_place(dev, ops, orc, dtype):
+    a, b = sample(orc, (6, 4), dtype), sample(orc, (4,), dtype, 2, 0.5, 2.0)
+    d, db = up(dev, a, dtype), up(dev, b, dtype)
+    ops.add_(d, db, alpha=0.5)
+    ops.mul__scalar(d, 2)
+    ops.sub_(d, db)
+    ops.div__scalar(d, 3)
+    ops.mul_(d, db)
+    ops.div_(d, db)
+    ops.add__scalar(d, 1.5, alpha=2)
+    want = orc.binary(ADD, dtype, a, b, 0.5)
+    want = orc.affine(dtype, want, 2.0, 0.0)
+    want = orc.binary(ADD, dtype, want, b, -1.0)
+    want = orc.affine(dtype, want, np.float32(1.0 / 3.0), 0.0)
+    want = orc.binary(MUL, dtype, want, b)
+    want = orc.binary(DIV, dtype, want, b)
+    want = orc.affine(dtype, want, 1.0, 3.0)
+    assert_elementwise(d.numpy(), want, dtype, "in-place chain", max_ulp=1)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_scalar_forms_of_strided_operands(dev, ops, orc, dtype):
+    base = sample(orc, (1, 5), dtype)
+    expanded = up(dev, base, dtype).expand(4, 5)
+    want = orc.affine(dtype, np.broadcast_to(base, (4, 5)).copy(), 3.0, 0.0)
+    assert_elementwise(ops.mul_scalar(expanded, 3).numpy(), want, dtype, "expanded * 3", max_ulp=1)
+    a = sample(orc, (6, 8), dtype)
+    d = up(dev, a, dtype)
+    ops.mul__scalar(d.t(), 0.5)
+    ops.add__scalar(d[:, ::2], 1.0)
+    want = orc.affine(dtype, a, 0.5, 0.0)
+    want[:, ::2] = orc.affine(dtype, np.ascontiguousarray(want[:, ::2]), 1.0, 1.0)
+    assert_elementwise(d.numpy(), want, dtype, "strided in-place", max_ulp=1)
+
+
+def test_strided_operands(dev, ops, orc):
+    a = sample(orc, (5, 7), F32)
+    d = up(dev, a, F32)
+    assert_bitexact(ops.add(d.t(), d.t()).numpy(), orc.binary(ADD, F32, a.T, a.T), "t + t")
+    got = ops.mul(d[:, ::2][:, :3], d[:, 1::2]).numpy()
+    assert_bitexact(got, orc.binary(MUL, F32, a[:, ::2][:, :3], a[:, 1::2]), "strided mul")
+
+
+def test_integer_math_is_declined(dev, ops):
+    tensor = __import__("importlib").import_module("tensorplay-mlu_amd.tensor")
+    x = dev.from_numpy(np.arange(10, dtype=np.int64))
+    with pytest.raises(tensor.DeclinedError):
+        ops.mul(x, x)
+    with pytest.raises(tensor.DeclinedError):
+        ops.mul_scalar(x, 3)
+
+
+UNARY = {  # name -> (oracle op code, input transform)
+    "exp": (0, None), "log": (1, "pos"), "sqrt": (2, "pos"), "rsqrt": (3, "pos"),
+    "neg": (4, None), "abs": (5, None), "relu": (8, None), "sigmoid": (9, None),
+    "tanh": (10, None), "silu": (11, None),
+}
+EXACT_UNARY = {"neg", "abs", "relu", "sqrt"}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("name", sorted(UNARY))
+def test_unary(dev, ops, orc, dtype, name):
+    code, transform = UNARY[name]
+    x = np.random.default_rng(3).standard_normal((33, 17)).astype(np.float32)
+    if transform == "pos":
+        x = np.abs(x) + 0.1
+    a = orc.from_float(x, dtype)
+    got = getattr(ops, name)(up(dev, a, dtype)).numpy()
+    want = orc.unary(code, dtype, a)
+    if name in EXACT_UNARY:
+        assert_bitexact(got, want, name)
+    else:
+        assert_elementwise(got, want, dtype, name)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("exponent", [2, 1, 0, 0.5, -0.5, 3, 1.7])
+def test_pow_scalar(dev, ops, orc, dtype, exponent):
+    x = np.abs(np.random.default_rng(4).standard_normal((6, 9)).astype(np.float32)) + 0.5
+    a = orc.from_float(x, dtype)
+    got = ops.pow_scalar(up(dev, a, dtype), exponent).numpy()
+    want = orc.unary(7, dtype, a, float(exponent))
+    assert_elementwise(got, want, dtype, f"pow {exponent}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_activations(dev, ops, orc, dtype):
+    a = sample(orc, (16, 32), dtype)
+    d = up(dev, a, dtype)
+    assert_elementwise(ops.gelu(d).numpy(), orc.unary(12, dtype, a), dtype, "gelu")
+    assert_elementwise(ops.gelu(d, "tanh").numpy(), orc.unary(13, dtype, a), dtype, "gelu tanh")
+    assert_elementwise(ops.silu(d).numpy(), orc.unary(11, dtype, a), dtype, "silu")
+    r = up(dev, a.copy(), dtype)
+    ops.relu_(r)
+    assert_bitexact(r.numpy(), orc.unary(8, dtype, a), "relu_")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_activation_backward(dev, ops, orc, dtype):
+    x = sample(orc, (37, 29), dtype, 5)
+    g = sample(orc, (37, 29), dtype, 6)
+    dx_, dg = up(dev, x, dtype), up(dev, g, dtype)
+    assert_bitexact(ops.threshold_backward(dg, dx_, 0).numpy(),
+                    orc.activation_backward(0, dtype, g, x, 0.0), "threshold_backward")
+    assert_bitexact(ops.threshold_backward(dg, dx_, 0.3).numpy(),
+                    orc.activation_backward(0, dtype, g, x, float(orc.to_float(orc.from_float(np.float32(0.3), dtype), dtype))),
+                    "threshold_backward 0.3")
+    y = orc.unary(9, dtype, x)
+    assert_elementwise(ops.sigmoid_backward(dg, up(dev, y, dtype)).numpy(),
+                       orc.activation_backward(1, dtype, g, y), dtype, "sigmoid_backward")
+    t = orc.unary(10, dtype, x)
+    assert_elementwise(ops.tanh_backward(dg, up(dev, t, dtype)).numpy(),
+                       orc.activation_backward(2, dtype, g, t), dtype, "tanh_backward")
+    assert_elementwise(ops.gelu_backward(dg, dx_).numpy(),
+                       orc.activation_backward(3, dtype, g, x), dtype, "gelu_backward")
+    assert_elementwise(ops.gelu_backward(dg, dx_, "tanh").numpy(),
+                       orc.activation_backward(4, dtype, g, x), dtype, "gelu_backward tanh")
+    assert_elementwise(ops.silu_backward(dg, dx_).numpy(),
+                       orc.activation_backward(5, dtype, g, x), dtype, "silu_backward")
+
+
+def test_large_narrow_float_elementwise(dev, ops, orc):
+    # The reference's 64 MiB narrow-float case (tests/test_mlu.py:336-341).
+    for dtype in (F16, BF16):
+        a = sample(orc, (4096, 8192), dtype)
+        d = up(dev, a, dtype)
+        assert_bitexact(ops.add(d, d).numpy(), orc.binary(ADD, dtype, a, a), "d + d")
+        assert_elementwise(ops.sigmoid(d).numpy(), orc.unary(9, dtype, a), dtype, "sigmoid")
+
+
+# ---- benchmark config 2 at full size ------------------------------------------------
+
+N = 8192
+
+
+@pytest.fixture(scope="module", params=[F32, BF16], ids=["fp32", "bf16"])
+def config2(request, dev, orc):
+    dtype = request.param
+    a = sample(orc, (N, N), dtype, 0)
+    row = sample(orc, (N,), dtype, 1, 0.5, 2.0)
+    col = sample(orc, (N, 1), dtype, 2, 0.5, 2.0)
+    g = sample(orc, (N, N), dtype, 3)
+    return dtype, a, row, col, g, up(dev, a, dtype), up(dev, row, dtype), up(dev, col, dtype), up(dev, g, dtype)
+
+
+def test_config2_binary_full_size(ops, orc, config2):
+    dtype, a, row, col, g, da, drow, dcol, dg = config2
+    for b, db, name in ((row, drow, "row"), (col, dcol, "col")):
+        assert_bitexact(ops.add(da, db).numpy(), orc.binary(ADD, dtype, a, b), f"add {name}")
+        assert_bitexact(ops.sub(da, db).numpy(), orc.binary(ADD, dtype, a, b, -1.0), f"sub {name}")
+        assert_bitexact(ops.mul(da, db).numpy(), orc.binary(MUL, dtype, a, b), f"mul {name}")
+        assert_bitexact(ops.div(da, db).numpy(), orc.binary(DIV, dtype, a, b), f"div {name}")
+    assert_elementwise(ops.mul_scalar(da, 1.5).numpy(), orc.affine(dtype, a, 1.5, 0.0), dtype,
+                       "mul scalar", max_ulp=1)
+    work = ops.clone(da)
+    ops.add_(work, drow, alpha=0.5)
+    assert_elementwise(work.numpy(), orc.binary(ADD, dtype, a, row, 0.5), dtype, "add_ row",
+                       max_ulp=1)
+
+
+def test_config2_unary_full_size(ops, orc, config2):
+    dtype, a, row, col, g, da, drow, dcol, dg = config2
+    assert_elementwise(ops.exp(da).numpy(), orc.unary(0, dtype, a), dtype, "exp")
+    absa = ops.abs(da)
+    shifted = ops.add_scalar(absa, 1e-3)
+    assert_elementwise(ops.log(shifted).numpy(), orc.unary(1, dtype, shifted.numpy()), dtype,
+                       "log(|a|+1e-3)")
+    assert_bitexact(ops.sqrt(absa).numpy(), orc.unary(2, dtype, absa.numpy()), "sqrt(|a|)")
+    assert_bitexact(ops.pow_scalar(da, 2).numpy(), orc.unary(6, dtype, a), "pow(a, 2)")
+    assert_bitexact(ops.relu(da).numpy(), orc.unary(8, dtype, a), "relu")
+    assert_elementwise(ops.gelu(da).numpy(), orc.unary(12, dtype, a), dtype, "gelu")
+    assert_elementwise(ops.sigmoid(da).numpy(), orc.unary(9, dtype, a), dtype, "sigmoid")
+
+
+def test_config2_backward_full_size(ops, orc, config2):
+    dtype, a, row, col, g, da, drow, dcol, dg = config2
+    assert_bitexact(ops.threshold_backward(dg, da, 0).numpy(),
+                    orc.activation_backward(0, dtype, g, a, 0.0), "relu backward")
+    assert_elementwise(ops.gelu_backward(dg, da).numpy(), orc.activation_backward(3, dtype, g, a),
+                       dtype, "gelu backward")
+    y = ops.sigmoid(da)
+    assert_elementwise(ops.sigmoid_backward(dg, y).numpy(),
+                       orc.activation_backward(1, dtype, g, y.numpy()), dtype, "sigmoid backward")

@@ -1,0 +1,188 @@
+"""Reductions and softmax on the GPU against the CPU oracle: the
+reference's cases (tests/test_mlu.py:303-350) and config 3 of the benchmark
+at full size.  amax/amin are bit-exact; sums, means and softmax use the
+reference's norm-wise rule (tests/_check.py)."""
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32, assert_bitexact, assert_normwise
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [F32, F16, BF16]
+SUM, MEAN, AMAX, AMIN = 0, 1, 2, 3
+
+
+def sample(orc, shape, dtype, seed=0, std=1.0):
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * np.float32(std)
+    return orc.from_float(x, dtype)
+
+
+def oracle_reduce(orc, op, dtype, x, dims, keepdim=False):
+    """Reduce over ``dims`` one run at a time with the oracle (float32
+    intermediates when the runs are not adjacent)."""
+    nd = x.ndim
+    dims = sorted(d % nd for d in (dims if dims else range(nd)))
+    shape = list(x.shape)
+    runs = []
+    for d in dims:
+        if runs and runs[-1][1] == d - 1:
+            runs[-1][1] = d
+        else:
+            runs.append([d, d])
+    cur, cur_dtype = x, dtype
+    if len(runs) > 1:
+        cur, cur_dtype = orc.to_float(x, dtype).astype(np.float32), F32
+    for first, last in reversed(runs):
+        outer = int(np.prod(shape[:first]))
+        r = int(np.prod(shape[first:last + 1]))
+        inner = int(np.prod(shape[last + 1:]))
+        cur = orc.reduce(op, cur_dtype, cur, outer, r, inner)
+        for d in range(first, last + 1):
+            shape[d] = 1
+        cur = cur.reshape(shape)
+    if len(runs) > 1:
+        cur = orc.from_float(cur, dtype)
+    if not keepdim:
+        cur = cur.reshape([s for i, s in enumerate(x.shape) if i not in dims])
+    return cur
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reductions(dev, ops, orc, dtype):
+    a = sample(orc, (6, 7, 8), dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    assert_normwise(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, 20, "sum")
+    assert_normwise(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, 5,
+                    "sum dim 1")
+    got = ops.sum_dim(d, (0, 2), keepdim=True).numpy()
+    assert got.shape == (1, 7, 1)
+    assert_normwise(got, oracle_reduce(orc, SUM, dtype, a, [0, 2], True), dtype, 20, "sum (0, 2)")
+    assert_normwise(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype, 1, "mean")
+    assert_normwise(ops.mean_dim(d, -1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [2]), dtype, 1,
+                    "mean dim -1")
+    for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
+        for dims in ([0], [1], [-1], [0, 2], []):
+            assert_bitexact(fn(d, dims).numpy(), oracle_reduce(orc, op, dtype, a, dims),
+                            f"amax/amin {dims}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_long_reductions(dev, ops, orc, dtype):
+    for shape in ((2, 4096), (2, 65536), (16, 8192), (3, 32768), (4096, 2)):
+        a = sample(orc, shape, dtype)
+        d = dev.from_numpy(a, dtype=dtype)
+        assert_normwise(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, 20)
+        assert_normwise(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype)
+        assert_normwise(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, 20)
+        assert_normwise(ops.mean_dim(d, 0).numpy(), oracle_reduce(orc, MEAN, dtype, a, [0]), dtype)
+        assert_bitexact(ops.amax(d, 0).numpy(), oracle_reduce(orc, AMAX, dtype, a, [0]), "amax 0")
+    a = sample(orc, (65537,), dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    assert_normwise(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, 20)
+    assert_bitexact(ops.amin(d).numpy(), oracle_reduce(orc, AMIN, dtype, a, None), "amin all")
+    a = sample(orc, (2, 4096, 2), dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    assert_normwise(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, 20)
+    assert_normwise(ops.mean_dim(d, 1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [1]), dtype)
+    a = sample(orc, (16, 8192), dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    assert_bitexact(ops.amax(d, -1).numpy(), oracle_reduce(orc, AMAX, dtype, a, [-1]), "amax -1")
+    assert_bitexact(ops.amin(d, -1).numpy(), oracle_reduce(orc, AMIN, dtype, a, [-1]), "amin -1")
+
+
+def test_reduction_edge_cases(dev, ops, orc):
+    # signed zeros and NaN: amax/amin skip NaN and order -0 below +0
+    x = np.array([[0.0, -0.0, np.nan], [-0.0, -0.0, np.nan], [np.nan, np.nan, np.nan],
+                  [1.0, np.nan, -2.0]], np.float32)
+    d = dev.from_numpy(x)
+    for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
+        got = fn(d, [1]).numpy()
+        want = orc.reduce(op, F32, x, 4, 3, 1)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        ok = ~np.isnan(want)
+        assert_bitexact(got[ok], want[ok], "signed zero / NaN")
+    # an empty reduced axis gives zeros (ReduceKernels.cpp:72-73)
+    e = dev.from_numpy(np.zeros((3, 0), np.float32))
+    assert_bitexact(ops.sum_dim(e, 1).numpy(), np.zeros(3, np.float32), "empty sum")
+    # a 0-d tensor reduces to itself
+    s = dev.from_numpy(np.array(2.5, np.float32))
+    assert ops.item(ops.sum(s)) == 2.5
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim", [0, 1, -1])
+def test_softmax_and_log_softmax(dev, ops, orc, dtype, dim):
+    a = sample(orc, (5, 6, 7), dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    k = dim % 3
+    outer, size, inner = int(np.prod(a.shape[:k])), a.shape[k], int(np.prod(a.shape[k + 1:]))
+    for log, fn in ((False, ops.softmax), (True, ops.log_softmax)):
+        y = fn(d, dim)
+        want = orc.softmax(log, dtype, a, outer, size, inner)
+        assert_normwise(y.numpy(), want, dtype, 1, f"softmax log={log}")
+        g = sample(orc, a.shape, dtype, 9)
+        back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
+        got = back(dev.from_numpy(g, dtype=dtype), y, dim, dtype).numpy()
+        assert_normwise(got, orc.softmax_backward(log, dtype, y.numpy(), g, outer, size, inner),
+                        dtype, 1, f"softmax backward log={log}")
+
+
+@pytest.mark.parametrize("D", [1, 7, 64, 256, 1000, 1024, 4096, 4100, 16384, 32000, 65536, 70000])
+def test_softmax_row_lengths(dev, ops, orc, D):
+    # every register-resident configuration and the two-read fallback
+    rows = max(1, min(64, (1 << 22) // D))
+    for dtype in (F32, BF16):
+        a = sample(orc, (rows, D), dtype, 1, 3.0)
+        d = dev.from_numpy(a, dtype=dtype)
+        for log in (False, True):
+            y = (ops.log_softmax if log else ops.softmax)(d, -1)
+            assert_normwise(y.numpy(), orc.softmax(log, dtype, a, rows, D, 1), dtype, 1,
+                            f"D={D} log={log}")
+            g = sample(orc, (rows, D), dtype, 2)
+            back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
+            got = back(dev.from_numpy(g, dtype=dtype), y, -1, dtype).numpy()
+            assert_normwise(got, orc.softmax_backward(log, dtype, y.numpy(), g, rows, D, 1),
+                            dtype, 1, f"backward D={D} log={log}")
+
+
+def test_softmax_declines(dev, ops, orc):
+    tensor = __import__("importlib").import_module("tensorplay-mlu_amd.tensor")
+    a = dev.from_numpy(sample(orc, (4, 5), F32))
+    with pytest.raises(tensor.DeclinedError):
+        ops._softmax(a, -1, True)  # half_to_float goes to the host (:202)
+    y = ops.softmax(a, -1)
+    with pytest.raises(tensor.DeclinedError):
+        ops._softmax_backward_data(a, y, -1, BF16)
+
+
+# ---- benchmark config 3 at full size ---------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape,std", [((32768, 4096), 2.0), ((4096, 32000), 4.0)],
+                         ids=["32768x4096", "4096x32000"])
+def test_config3_full_size(dev, ops, orc, dtype, shape, std):
+    a = sample(orc, shape, dtype, 0, std)
+    d = dev.from_numpy(a, dtype=dtype)
+    R, C = shape
+    for dim, (outer, r, inner) in ((-1, (R, C, 1)), (0, (1, R, C))):
+        assert_normwise(ops.sum_dim(d, dim).numpy(), orc.reduce(SUM, dtype, a, outer, r, inner),
+                        dtype, 20, f"sum dim {dim}")
+        assert_normwise(ops.mean_dim(d, dim).numpy(), orc.reduce(MEAN, dtype, a, outer, r, inner),
+                        dtype, 1, f"mean dim {dim}")
+        assert_bitexact(ops.amax(d, dim).numpy(), orc.reduce(AMAX, dtype, a, outer, r, inner),
+                        f"amax dim {dim}")
+        assert_bitexact(ops.amin(d, dim).numpy(), orc.reduce(AMIN, dtype, a, outer, r, inner),
+                        f"amin dim {dim}")
+    g = sample(orc, shape, dtype, 1)
+    dg = dev.from_numpy(g, dtype=dtype)
+    for log in (False, True):
+        y = (ops.log_softmax if log else ops.softmax)(d, -1)
+        yh = y.numpy()
+        assert_normwise(yh, orc.softmax(log, dtype, a, R, C, 1), dtype, 1, f"softmax log={log}")
+        back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
+        assert_normwise(back(dg, y, -1, dtype).numpy(),
+                        orc.softmax_backward(log, dtype, yh, g, R, C, 1), dtype, 1,
+                        f"softmax backward log={log}")
