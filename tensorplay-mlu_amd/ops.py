@@ -34,7 +34,7 @@ def _ref(x):
             arr = arr.astype(np.float32)  # a Python float is a float32 host scalar
         if arr.dtype == np.int64 and isinstance(x, bool):
             arr = arr.astype(np.bool_)
-        arr = np.ascontiguousarray(arr)
+        arr = np.asarray(arr, order="C")
         _keep.append(arr)
         return C.byref(host_view(arr))
     raise TypeError(f"unsupported operand {type(x)}")

@@ -123,7 +123,7 @@ class DeviceTensor:
     def from_numpy(array: np.ndarray, device: int = 0, dtype=None) -> "DeviceTensor":
         """Copy a host array to the device.  ``dtype="bfloat16"`` reads
         ``array`` as uint16 bit patterns."""
-        array = np.ascontiguousarray(array)
+        array = np.asarray(array, order="C")
         code = dtype_code(dtype) if dtype is not None else NP_TO_CODE[array.dtype]
         if code == _abi.BFLOAT16:
             array = array.view(np.uint16) if array.dtype.itemsize == 2 else array

@@ -175,7 +175,7 @@ def test_activation_backward(dev, ops, orc, dtype):
     assert_bitexact(ops.threshold_backward(dg, dx_, 0).numpy(),
                     orc.activation_backward(0, dtype, g, x, 0.0), "threshold_backward")
     assert_bitexact(ops.threshold_backward(dg, dx_, 0.3).numpy(),
-                    orc.activation_backward(0, dtype, g, x, float(orc.to_float(orc.from_float(np.float32(0.3), dtype), dtype))),
+                    orc.activation_backward(0, dtype, g, x, float(orc.to_float(orc.from_float(np.float32([0.3]), dtype), dtype)[0])),
                     "threshold_backward 0.3")
     y = orc.unary(9, dtype, x)
     assert_elementwise(ops.sigmoid_backward(dg, up(dev, y, dtype)).numpy(),
