@@ -196,6 +196,47 @@ def suite_config3(ops, dev, ev):
     return out
 
 
+def suite_gemm(ops, dev, ev):
+    """Configs 4 and 5a: matrix products (TFLOP/s against the dtype's dense
+    MFMA peak; bmm also against HBM)."""
+    out = {}
+    g = np.random.default_rng(0)
+
+    def put(shape, dtype, scale):
+        d = dev.from_numpy(g.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+        return d if dtype == F32 else ops.to(d, dtype)
+
+    def record(name, fn, flops, dtype, nbytes=None):
+        for _ in range(2):
+            fn()
+        ms = ev.time_ms(fn, 5)
+        tf = flops / (ms * 1e-3) / 1e12
+        peak = MFMA_PEAK_TFLOPS[NAME[dtype]]
+        entry = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / peak, 4)}
+        if nbytes is not None:
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            entry.update({"GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)})
+        out[f"{name}_{NAME[dtype]}"] = entry
+
+    for dtype in (BF16, F32):
+        K = 4096
+        a, b = put((K, K), dtype, K ** -0.25), put((K, K), dtype, K ** -0.25)
+        bias = put((K,), dtype, 1.0)
+        at = ops.contiguous(a.t())
+        record("mm_4096", lambda: ops.mm(a, b), 2 * K ** 3, dtype)
+        record("addmm_4096", lambda: ops.addmm(bias, a, b), 2 * K ** 3, dtype)
+        record("mm_4096_At", lambda: ops.mm(at.t(), b), 2 * K ** 3, dtype)
+        del a, b, at
+        x, w = put((8192, 4096), dtype, 4096 ** -0.25), put((11008, 4096), dtype, 4096 ** -0.25)
+        lb = put((11008,), dtype, 1.0)
+        record("linear_8192x4096x11008", lambda: ops.linear(x, w, lb), 2 * 8192 * 11008 * 4096, dtype)
+        del x, w
+    a, b = put((64, 512, 128), BF16, 128 ** -0.25), put((64, 128, 512), BF16, 128 ** -0.25)
+    record("bmm_64x512x128x512", lambda: ops.bmm(a, b), 2 * 64 * 512 * 512 * 128, BF16,
+           nbytes=(64 * 512 * 128 * 2 + 64 * 512 * 512) * 2)
+    return out
+
+
 def cpu_baseline(rows: int = 1024):
     """The C oracle (CPU port, float64 arithmetic, OpenMP) on the first
     ``rows`` rows of config 2, both dtypes; GB/s of algorithmic bytes."""
@@ -305,6 +346,8 @@ def main() -> int:
         del tensors
         log("bench: suite config 3")
         suite["config3"] = suite_config3(ops, dev, ev)
+        log("bench: suite configs 4 and 5a")
+        suite["config4_5a"] = suite_gemm(ops, dev, ev)
         result["suite"] = suite
     if not args.no_cpu:
         log("bench: cpu baseline")

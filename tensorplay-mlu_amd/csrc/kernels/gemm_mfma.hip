@@ -1,0 +1,337 @@
+// Matrix-core GEMM for gfx950 (CDNA4), and the dispatch between it and the
+// general kernel (gemm.hip).
+//
+// C[b] = alpha * op(A[b]) op(B[b]) + beta * Cin[b] with float32
+// accumulation on MFMA:
+//   * bfloat16 / float16: v_mfma_f32_32x32x16_{bf16,f16} -- each lane feeds
+//     8 consecutive k of one row of A and of one column of B;
+//   * float32: v_mfma_f32_32x32x2_f32 -- each lane feeds one k; a 16-byte
+//     LDS read gives a lane 4 consecutive k that feed 4 back-to-back MFMAs
+//     (lane half h supplies k = 4h + j to MFMA j, for A and B alike, so the
+//     pairing of A and B elements is exact whatever order the sum takes).
+// Block tile BM x BN, 4 waves in a 2 x 2 grid each owning a 64 x 64 patch
+// (2 x 2 MFMA tiles of 32 x 32); K advances BK at a time.  Both operands are
+// staged in LDS K-major ([row][k], rows padded by 16 bytes so the 16-byte
+// fragment reads of 16 consecutive rows hit distinct banks).  An operand
+// stored K-major in memory is copied with 16-byte loads; one stored with its
+// M (or N) axis contiguous -- a transposed view, read in place -- is loaded
+// as V x 4 blocks (V along M/N, 4 along K) and transposed in registers before
+// its LDS store.  The next K tile's global loads are issued before the MFMAs
+// of the current one, so their latency hides behind the math.  Tiles are
+// numbered so each of the 8 XCDs walks a contiguous range in groups of 8 tile
+// rows, keeping an XCD's B (and A) panels hot in its own L2.
+
+#include "device_common.h"
+#include "gemm.h"
+#include "../common.h"
+
+namespace tp_amd {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<bf16_t> {
+    static constexpr int V = 8;     // elements per 16-byte vector
+    static constexpr int BK = 64;   // K per LDS tile
+    static constexpr int KSUB = 16; // K per fragment read
+    __device__ __forceinline__ static f32x16 mma(const uint4& a, const uint4& b, f32x16 c) {
+        bf16x8 av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<f16_t> {
+    static constexpr int V = 8;
+    static constexpr int BK = 64;
+    static constexpr int KSUB = 16;
+    __device__ __forceinline__ static f32x16 mma(const uint4& a, const uint4& b, f32x16 c) {
+        f16x8 av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<float> {
+    static constexpr int V = 4;
+    static constexpr int BK = 32;
+    static constexpr int KSUB = 8;
+    __device__ __forceinline__ static f32x16 mma(const uint4& a, const uint4& b, f32x16 c) {
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+        return c;
+    }
+};
+
+constexpr int kThreads = 256;
+constexpr int kBM = 128, kBN = 128;
+constexpr int kWaveM = 64, kWaveN = 64;  // per-wave patch
+constexpr int kGroupM = 8;
+
+// One operand's tile loader: R rows (M or N) x BK, into LDS [R][BK + pad].
+// KMAJOR: element (r, k) at X[r * ld + k]; otherwise at X[k * ld + r].
+template <typename T, int R, bool KMAJOR>
+struct TileLoader {
+    using S = typename Elem<T>::storage;
+    static constexpr int V = Mfma<T>::V;
+    static constexpr int BK = Mfma<T>::BK;
+    static constexpr int LDS_STRIDE = BK + 16 / sizeof(S);  // elements per LDS row
+    // K-major: R * BK / V vectors; MN-major: (R / V) * (BK / 4) units of 4 vectors.
+    static constexpr int kLoads = 4;
+    static_assert((KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) == kLoads * kThreads,
+                  "tile shape and thread count disagree");
+    uint4 reg[kLoads];
+
+    __device__ __forceinline__ void load(const S* X, int64_t ld, int64_t r0, int64_t rows,
+                                         int64_t k0, int64_t K) {
+        const int tid = threadIdx.x;
+        if constexpr (KMAJOR) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int v = tid + i * kThreads;
+                const int r = v / (BK / V), kc = v % (BK / V);
+                const int64_t gr = r0 + r, gk = k0 + kc * V;
+                if (gr < rows && gk < K) {
+                    reg[i] = *reinterpret_cast<const uint4*>(X + gr * ld + gk);
+                } else {
+                    reg[i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        } else {
+            const int rb = tid % (R / V), kb = tid / (R / V);
+            const int64_t gr = r0 + rb * V;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t gk = k0 + kb * 4 + i;
+                if (gr < rows && gk < K) {
+                    reg[i] = *reinterpret_cast<const uint4*>(X + gk * ld + gr);
+                } else {
+                    reg[i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(S* lds) const {
+        const int tid = threadIdx.x;
+        if constexpr (KMAJOR) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int v = tid + i * kThreads;
+                const int r = v / (BK / V), kc = v % (BK / V);
+                *reinterpret_cast<uint4*>(lds + r * LDS_STRIDE + kc * V) = reg[i];
+            }
+        } else {
+            const int rb = tid % (R / V), kb = tid / (R / V);
+            if constexpr (sizeof(S) == 4) {
+                // 4 (k) x 4 (r) floats -> 4 rows of 4 consecutive k.
+                const uint32_t* in = reinterpret_cast<const uint32_t*>(reg);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint4 out = make_uint4(in[0 * 4 + j], in[1 * 4 + j], in[2 * 4 + j],
+                                                 in[3 * 4 + j]);
+                    *reinterpret_cast<uint4*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
+                }
+            } else {
+                // 4 (k) x 8 (r) 16-bit values -> 8 rows of 4 consecutive k.
+                const uint32_t* in = reinterpret_cast<const uint32_t*>(reg);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int p = j / 2, hi = j % 2;
+                    uint32_t w[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) w[i] = hi ? (in[i * 4 + p] >> 16) : (in[i * 4 + p] & 0xffffu);
+                    uint2 out;
+                    out.x = w[0] | (w[1] << 16);
+                    out.y = w[2] | (w[3] << 16);
+                    *reinterpret_cast<uint2*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
+                }
+            }
+        }
+    }
+};
+
+// XCD-aware, L2-grouped tile order: consecutive ids land on the same XCD
+// (blocks are dealt round-robin over the 8 XCDs), and each XCD walks its
+// range in groups of kGroupM tile rows.
+__device__ __forceinline__ void tile_coords(int bid, int grid_m, int grid_n, int& pm, int& pn) {
+    const int total = grid_m * grid_n;
+    int pid = bid;
+    if (total % 8 == 0) pid = (bid % 8) * (total / 8) + bid / 8;
+    const int in_group = kGroupM * grid_n;
+    const int group = pid / in_group;
+    const int first_m = group * kGroupM;
+    const int size_m = grid_m - first_m < kGroupM ? grid_m - first_m : kGroupM;
+    pm = first_m + (pid % in_group) % size_m;
+    pn = (pid % in_group) / size_m;
+}
+
+template <typename T, bool A_KMAJOR, bool B_KMAJOR>
+__global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
+    using S = typename Elem<T>::storage;
+    using LA = TileLoader<T, kBM, A_KMAJOR>;
+    using LB = TileLoader<T, kBN, B_KMAJOR>;
+    constexpr int BK = Mfma<T>::BK, KSUB = Mfma<T>::KSUB;
+    constexpr int LDS_STRIDE = LA::LDS_STRIDE;
+    constexpr int TM = kWaveM / 32, TN = kWaveN / 32;
+    __shared__ __attribute__((aligned(16))) S As[kBM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) S Bs[kBN * LDS_STRIDE];
+
+    const int grid_m = static_cast<int>((p.m + kBM - 1) / kBM);
+    const int grid_n = static_cast<int>((p.n + kBN - 1) / kBN);
+    int pm, pn;
+    tile_coords(blockIdx.x, grid_m, grid_n, pm, pn);
+    const int64_t m0 = static_cast<int64_t>(pm) * kBM, n0 = static_cast<int64_t>(pn) * kBN;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wm = wave / 2, wn = wave % 2;
+    const int half = lane / 32, l32 = lane % 32;
+
+    for (int64_t bi = blockIdx.z; bi < p.batch; bi += gridDim.z) {
+        const S* A = static_cast<const S*>(p.a) + bi * p.stride_a;
+        const S* B = static_cast<const S*>(p.b) + bi * p.stride_b;
+        f32x16 acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+        LA la;
+        LB lb;
+        la.load(A, p.lda, m0, p.m, 0, p.k);
+        lb.load(B, p.ldb, n0, p.n, 0, p.k);
+        for (int64_t k0 = 0; k0 < p.k; k0 += BK) {
+            la.store(As);
+            lb.store(Bs);
+            __syncthreads();
+            if (k0 + BK < p.k) {
+                la.load(A, p.lda, m0, p.m, k0 + BK, p.k);
+                lb.load(B, p.ldb, n0, p.n, k0 + BK, p.k);
+            }
+#pragma unroll
+            for (int s = 0; s < BK / KSUB; ++s) {
+                uint4 af[TM], bf[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int row = wm * kWaveM + i * 32 + l32;
+                    af[i] = *reinterpret_cast<const uint4*>(As + row * LDS_STRIDE + s * KSUB +
+                                                            half * (KSUB / 2));
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = wn * kWaveN + j * 32 + l32;
+                    bf[j] = *reinterpret_cast<const uint4*>(Bs + col * LDS_STRIDE + s * KSUB +
+                                                            half * (KSUB / 2));
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[i], bf[j], acc[i][j]);
+            }
+            __syncthreads();
+        }
+
+        // Epilogue: lane holds column l32 of each 32 x 32 tile, rows
+        // 8 * (e / 4) + 4 * half + e % 4 for accumulator element e.
+        S* C = static_cast<S*>(p.c) + bi * p.stride_c;
+        const S* Cin = static_cast<const S*>(p.cin);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t col = n0 + wn * kWaveN + j * 32 + l32;
+                const int64_t rbase = m0 + wm * kWaveM + i * 32 + 4 * half;
+                if (col >= p.n) continue;
+                S* cp = C + rbase * p.ldc + col;
+                if (p.beta == 0.0f) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (rbase + 8 * g + r < p.m) {
+                                cp[r * p.ldc] = Elem<T>::store(p.alpha * acc[i][j][4 * g + r]);
+                            }
+                        }
+                        cp += 8 * p.ldc;
+                    }
+                } else {
+                    const S* ci = Cin + bi * p.cin_stride_b + rbase * p.cin_rs + col * p.cin_cs;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (rbase + 8 * g + r < p.m) {
+                                const float c = Elem<T>::load(ci[r * p.cin_rs]);
+                                cp[r * p.ldc] =
+                                    Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r]));
+                            }
+                        }
+                        cp += 8 * p.ldc;
+                        ci += 8 * p.cin_rs;
+                    }
+                }
+            }
+    }
+}
+
+template <typename T>
+bool mfma_eligible(const GemmArgs& p) {
+    constexpr int V = Mfma<T>::V;
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    auto ok = [&](const void* ptr, int64_t ld, int64_t stride, bool kmajor, int64_t mn) {
+        return aligned16(ptr) && ld % V == 0 && stride % V == 0 && (kmajor ? p.k % V == 0 : mn % V == 0);
+    };
+    return p.k > 0 && ok(p.a, p.lda, p.stride_a, a_kmajor, p.m) &&
+           ok(p.b, p.ldb, p.stride_b, b_kmajor, p.n) &&
+           (p.m + kBM - 1) / kBM * ((p.n + kBN - 1) / kBN) < (int64_t(1) << 31);
+}
+
+template <typename T>
+void launch_mfma(const GemmArgs& p, hipStream_t stream) {
+    const int64_t tiles = ((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
+    const dim3 grid(static_cast<unsigned>(tiles), 1u,
+                    static_cast<unsigned>(p.batch < 65535 ? p.batch : 65535));
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    if (a_kmajor && b_kmajor) gemm_mfma_kernel<T, true, true><<<grid, kThreads, 0, stream>>>(p);
+    else if (a_kmajor) gemm_mfma_kernel<T, true, false><<<grid, kThreads, 0, stream>>>(p);
+    else if (b_kmajor) gemm_mfma_kernel<T, false, true><<<grid, kThreads, 0, stream>>>(p);
+    else gemm_mfma_kernel<T, false, false><<<grid, kThreads, 0, stream>>>(p);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+template <typename T>
+void launch_typed(const GemmArgs& p, hipStream_t stream) {
+    if (mfma_eligible<T>(p)) {
+        launch_mfma<T>(p, stream);
+    } else {
+        launch_gemm_general<T>(p, stream);
+    }
+}
+
+}  // namespace
+
+void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream) {
+    switch (dtype) {
+        case TP_AMD_FLOAT32: launch_typed<float>(p, stream); break;
+        case TP_AMD_BFLOAT16: launch_typed<bf16_t>(p, stream); break;
+        case TP_AMD_FLOAT16: launch_typed<f16_t>(p, stream); break;
+        default:
+            TP_AMD_CHECK(false, "GEMM takes float32, float16 or bfloat16, got ", dtype_name(dtype));
+    }
+}
+
+}  // namespace tp_amd

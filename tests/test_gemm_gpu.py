@@ -1,0 +1,198 @@
+"""Matrix products on the GPU against the CPU oracle: the reference's cases
+(tests/test_mlu.py:238-300) and configs 4 and 5a of the benchmark at full
+size.
+
+Bars (north_star): float32 products within 2e-3 and bfloat16 / float16
+products (float32 accumulation) within 1e-2, both as max |got - want| /
+max |want| against the float64 product of the same stored inputs.  Full-size
+products are checked on 4096 sampled entries computed exactly by the oracle
+and, over the whole matrix, with Freivalds' test C x = A (B x) in float64.
+"""
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [F32, BF16, F16]
+BAR = {F32: 2e-3, BF16: 1e-2, F16: 1e-2}
+
+
+def sample(orc, shape, dtype, seed, scale=1.0):
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * np.float32(scale)
+    return orc.from_float(x, dtype)
+
+
+def rel_err(orc, got, want, dtype):
+    g = orc.to_float(got, dtype)
+    w = orc.to_float(want, dtype) if want.dtype != np.float64 else want
+    return float(np.max(np.abs(g - w)) / max(np.max(np.abs(w)), 1e-30))
+
+
+def check(orc, got, want, dtype, what):
+    e = rel_err(orc, got, want, dtype)
+    assert e <= BAR[dtype], f"{what}: relative error {e:.3g} > {BAR[dtype]}"
+    return e
+
+
+def exact(orc, a, b, dtype, ta=False, tb=False):
+    """float64 product of the stored operands (op = transpose when t*)."""
+    A = orc.to_float(a, dtype)
+    B = orc.to_float(b, dtype)
+    A = np.swapaxes(A, -1, -2) if ta else A
+    B = np.swapaxes(B, -1, -2) if tb else B
+    return A @ B
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(37, 19, 23), (128, 64, 96), (200, 72, 136), (256, 256, 256),
+                                   (64, 520, 24), (8, 16, 8)])
+def test_mm_transposes(dev, ops, orc, dtype, ta, tb, m, k, n):
+    a = sample(orc, (k, m) if ta else (m, k), dtype, 1)
+    b = sample(orc, (n, k) if tb else (k, n), dtype, 3)
+    da = dev.from_numpy(a, dtype=dtype)
+    db = dev.from_numpy(b, dtype=dtype)
+    got = ops.mm(da.t() if ta else da, db.t() if tb else db).numpy()
+    want = orc.gemm(dtype, a, b, ta, tb)
+    assert got.shape == (m, n)
+    check(orc, got, want, dtype, f"mm ta={ta} tb={tb}")
+    check(orc, got, exact(orc, a, b, dtype, ta, tb), dtype, "mm vs float64")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_addmm_bmm_matmul(dev, ops, orc, dtype):
+    bias, a, b = sample(orc, (23,), dtype, 0), sample(orc, (37, 19), dtype, 1), sample(orc, (19, 23), dtype, 2)
+    d = lambda x: dev.from_numpy(x, dtype=dtype)  # noqa: E731
+    got = ops.addmm(d(bias), d(a), d(b), beta=0.5, alpha=2.0).numpy()
+    check(orc, got, orc.gemm(dtype, a, b, alpha=2.0, beta=0.5, cin=bias), dtype, "addmm")
+    want64 = 0.5 * orc.to_float(bias, dtype) + 2.0 * exact(orc, a, b, dtype)
+    check(orc, got, want64, dtype, "addmm vs float64")
+    x, y = sample(orc, (4, 9, 6), dtype, 4), sample(orc, (4, 6, 5), dtype, 5)
+    check(orc, ops.bmm(d(x), d(y)).numpy(), orc.gemm(dtype, x, y), dtype, "bmm")
+    w = sample(orc, (6, 5), dtype, 6)
+    got = ops.matmul(d(x), d(w)).numpy()
+    assert got.shape == (4, 9, 5)
+    check(orc, got, exact(orc, x, w, dtype), dtype, "matmul 3d @ 2d")
+    v = sample(orc, (2, 1, 6, 3), dtype, 7)
+    got = ops.matmul(d(x), d(v)).numpy()
+    assert got.shape == (2, 4, 9, 3)
+    check(orc, got, exact(orc, x, v, dtype), dtype, "matmul broadcast batch")
+    u = sample(orc, (6,), dtype, 8)
+    got = ops.matmul(d(x), d(u)).numpy()
+    assert got.shape == (4, 9)
+    check(orc, got, exact(orc, x, u, dtype), dtype, "matmul 3d @ 1d")
+    got = ops.matmul(d(u), d(w)).numpy()
+    assert got.shape == (5,)
+    check(orc, got, exact(orc, u, w, dtype), dtype, "matmul 1d @ 2d")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear(dev, ops, orc, dtype):
+    x, w, b = sample(orc, (3, 5, 64), dtype, 0), sample(orc, (48, 64), dtype, 1), sample(orc, (48,), dtype, 2)
+    d = lambda t: dev.from_numpy(t, dtype=dtype)  # noqa: E731
+    want = exact(orc, x, w, dtype, tb=True)
+    got = ops.linear(d(x), d(w), d(b)).numpy()
+    assert got.shape == (3, 5, 48)
+    check(orc, got, want + orc.to_float(b, dtype), dtype, "linear with bias")
+    check(orc, ops.linear(d(x), d(w)).numpy(), want, dtype, "linear")
+    got = ops.linear(d(x)[0, 0], d(w), d(b)).numpy()
+    assert got.shape == (48,)
+    check(orc, got, want[0, 0] + orc.to_float(b, dtype), dtype, "linear 1-d input")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bmm_shapes(dev, ops, orc, dtype):
+    for (bt, m, k, n) in ((32, 512, 64, 512), (1, 256, 4096, 1024), (3, 1, 7, 5)):
+        a = sample(orc, (bt, m, k), dtype, 1, k ** -0.5)
+        b = sample(orc, (bt, k, n), dtype, 2)
+        got = ops.bmm(dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)).numpy()
+        check(orc, got, exact(orc, a, b, dtype), dtype, f"bmm {bt}x{m}x{k}x{n}")
+    a, b = sample(orc, (4, 9, 6), dtype, 3), sample(orc, (4, 5, 6), dtype, 4)
+    got = ops.bmm(dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype).transpose(1, 2)).numpy()
+    check(orc, got, exact(orc, a, b, dtype, tb=True), dtype, "bmm transposed operand")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,k,n", [(2, 1024, 1024), (128, 1024, 256), (256, 4096, 1024),
+                                   (1024, 4096, 128)])
+def test_mm_shapes(dev, ops, orc, dtype, m, k, n):
+    a, b = sample(orc, (m, k), dtype, 1), sample(orc, (k, n), dtype, 2)
+    got = ops.mm(dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)).numpy()
+    check(orc, got, exact(orc, a, b, dtype), dtype, f"mm {m}x{k}x{n}")
+
+
+def test_k_zero_and_empty(dev, ops, orc):
+    a = dev.from_numpy(np.zeros((4, 0), np.float32))
+    b = dev.from_numpy(np.zeros((0, 3), np.float32))
+    assert np.array_equal(ops.mm(a, b).numpy(), np.zeros((4, 3), np.float32))
+    bias = dev.from_numpy(np.arange(3, dtype=np.float32))
+    got = ops.addmm(bias, a, b, beta=2.0).numpy()
+    assert np.array_equal(got, np.broadcast_to(np.arange(3, dtype=np.float32) * 2, (4, 3)))
+
+
+# ---- full-size configs ------------------------------------------------------------
+
+
+def sampled_entries(orc, got, a, b, dtype, ta=False, tb=False, alpha=1.0, beta=0.0, cin=None,
+                    count=4096, seed=0):
+    m, n = got.shape[-2:]
+    g = np.random.default_rng(seed)
+    idx = np.stack([np.zeros(count, np.int64), g.integers(0, m, count), g.integers(0, n, count)], 1)
+    want = orc.gemm_entries(dtype, a, b, idx, ta, tb, alpha, beta, cin)
+    have = orc.to_float(got, dtype)[idx[:, 1], idx[:, 2]]
+    return float(np.max(np.abs(have - want)) / np.max(np.abs(want)))
+
+
+def freivalds(orc, got, a, b, dtype, ta=False, tb=False, bias=None):
+    """max |C x - A (B x)| relative to max |A (B x)|, in float64."""
+    x = np.random.default_rng(7).standard_normal(got.shape[-1])
+    A = orc.to_float(a, dtype)
+    B = orc.to_float(b, dtype)
+    A = A.T if ta else A
+    B = B.T if tb else B
+    ref = A @ (B @ x)
+    if bias is not None:
+        ref = ref + float(orc.to_float(bias, dtype) @ x)
+    lhs = orc.to_float(got, dtype) @ x
+    return float(np.max(np.abs(lhs - ref)) / np.max(np.abs(ref)))
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_config4_mm_4096(dev, ops, orc, dtype):
+    K = 4096
+    a = sample(orc, (K, K), dtype, 1, K ** -0.25)
+    b = sample(orc, (K, K), dtype, 2, K ** -0.25)
+    da, db = dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)
+    got = ops.mm(da, db).numpy()
+    assert sampled_entries(orc, got, a, b, dtype) <= BAR[dtype]
+    assert freivalds(orc, got, a, b, dtype) <= BAR[dtype]
+    # A stored [K, M] and read in place through .t()
+    at = np.ascontiguousarray(a.T)
+    got_t = ops.mm(dev.from_numpy(at, dtype=dtype).t(), db).numpy()
+    assert sampled_entries(orc, got_t, at, b, dtype, ta=True) <= BAR[dtype]
+    # addmm with a [4096] bias
+    bias = sample(orc, (K,), dtype, 3)
+    got_b = ops.addmm(dev.from_numpy(bias, dtype=dtype), da, db).numpy()
+    assert sampled_entries(orc, got_b, a, b, dtype, beta=1.0, cin=bias) <= BAR[dtype]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_config4_linear(dev, ops, orc, dtype):
+    x = sample(orc, (8192, 4096), dtype, 1, 4096 ** -0.25)
+    w = sample(orc, (11008, 4096), dtype, 2, 4096 ** -0.25)
+    b = sample(orc, (11008,), dtype, 3)
+    got = ops.linear(dev.from_numpy(x, dtype=dtype), dev.from_numpy(w, dtype=dtype),
+                     dev.from_numpy(b, dtype=dtype)).numpy()
+    assert got.shape == (8192, 11008)
+    assert sampled_entries(orc, got, x, w, dtype, tb=True, beta=1.0, cin=b) <= BAR[dtype]
+    assert freivalds(orc, got, x, w, dtype, tb=True, bias=b) <= BAR[dtype]
+
+
+def test_config5_bmm_bf16(dev, ops, orc):
+    a = sample(orc, (64, 512, 128), BF16, 1, 128 ** -0.25)
+    b = sample(orc, (64, 128, 512), BF16, 2, 128 ** -0.25)
+    got = ops.bmm(dev.from_numpy(a, dtype=BF16), dev.from_numpy(b, dtype=BF16)).numpy()
+    check(orc, got, exact(orc, a, b, BF16), BF16, "bmm 64x512x128x512")
