@@ -171,7 +171,9 @@ static double unary_value(int op, double x, double p) {
         case 10: return tanh(x);
         case 11: return x / (1.0 + exp(-x));                /* silu */
         case 12: return 0.5 * x * erfc(-x / sqrt(2.0));     /* gelu, erf form */
-        default: return 0.5 * x * (1.0 + tanh(kSqrt2OverPi * (x + kGeluC * x * x * x)));
+        /* gelu, tanh form: 0.5 x (1 + tanh u) = x / (1 + exp(-2u)) exactly; the
+         * second form keeps full relative accuracy for large negative x */
+        default: return x / (1.0 + exp(-2.0 * kSqrt2OverPi * (x + kGeluC * x * x * x)));
     }
 }
 
@@ -193,10 +195,11 @@ static double backward_value(int op, double g, double s, double p) {
             return g * (cdf + s * pdf);
         }
         case 4: {
+            /* d/dx [x sigmoid(2u)] with the same stable sigmoid */
             const double u = kSqrt2OverPi * (s + kGeluC * s * s * s);
-            const double t = tanh(u);
+            const double sg = 1.0 / (1.0 + exp(-2.0 * u));
             const double du = kSqrt2OverPi * (1.0 + 3.0 * kGeluC * s * s);
-            return g * (0.5 * (1.0 + t) + 0.5 * s * (1.0 - t * t) * du);
+            return g * (sg + 2.0 * s * sg * (1.0 - sg) * du);
         }
         default: {
             const double sg = 1.0 / (1.0 + exp(-s));
