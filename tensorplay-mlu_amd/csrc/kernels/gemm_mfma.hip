@@ -9,21 +9,25 @@
 //     LDS read gives a lane 4 consecutive k that feed 4 back-to-back MFMAs
 //     (lane half h supplies k = 4h + j to MFMA j, for A and B alike, so the
 //     pairing of A and B elements is exact whatever order the sum takes).
-// Block tile BM x BN, 4 waves in a 2 x 2 grid each owning a 64 x 64 patch
-// (2 x 2 MFMA tiles of 32 x 32); K advances BK at a time.  Both operands are
-// staged in LDS K-major ([row][k], rows padded by 16 bytes so the 16-byte
-// fragment reads of 16 consecutive rows hit distinct banks).  An operand
-// stored K-major in memory is copied with 16-byte loads; one stored with its
-// M (or N) axis contiguous -- a transposed view, read in place -- is loaded
-// as V x 4 blocks (V along M/N, 4 along K) and transposed in registers before
-// its LDS store.  The next K tile's global loads are issued before the MFMAs
-// of the current one, so their latency hides behind the math.  Tiles are
-// numbered so each of the 8 XCDs walks a contiguous range in groups of 8 tile
-// rows, keeping an XCD's B (and A) panels hot in its own L2.
+// Two block shapes: 256 x 256 with 8 waves (2 x 4, each wave a 128 x 64
+// patch of 4 x 2 MFMA tiles of 32 x 32) for large problems, and 128 x 128
+// with 4 waves (2 x 2, each 64 x 64) when the big tiles would leave CUs idle.
+// K advances BK at a time through two LDS stages: while the waves multiply
+// out of one stage, the next K tile is written into the other and the one
+// after is already in flight from global memory, so each K step needs a
+// single barrier.  Operands sit in LDS K-major ([row][k], rows padded by 16
+// bytes so the 16-byte fragment reads of 16 consecutive rows hit distinct
+// banks).  An operand stored K-major in memory is copied with 16-byte loads;
+// one stored with its M (or N) axis contiguous -- a transposed view, read in
+// place -- is loaded as V x 4 blocks (V along M/N, 4 along K) and transposed
+// in registers before its LDS store.  Tiles are numbered so each of the 8
+// XCDs walks a contiguous range in groups of 8 tile rows, keeping an XCD's A
+// and B panels hot in its own L2.
 
 #include "device_common.h"
 #include "gemm.h"
 #include "../common.h"
+#include "../runtime.h"
 
 namespace tp_amd {
 
@@ -76,14 +80,11 @@ struct Mfma<float> {
     }
 };
 
-constexpr int kThreads = 256;
-constexpr int kBM = 128, kBN = 128;
-constexpr int kWaveM = 64, kWaveN = 64;  // per-wave patch
 constexpr int kGroupM = 8;
 
 // One operand's tile loader: R rows (M or N) x BK, into LDS [R][BK + pad].
 // KMAJOR: element (r, k) at X[r * ld + k]; otherwise at X[k * ld + r].
-template <typename T, int R, bool KMAJOR>
+template <typename T, int R, bool KMAJOR, int THREADS>
 struct TileLoader {
     using S = typename Elem<T>::storage;
     static constexpr int V = Mfma<T>::V;
@@ -91,7 +92,7 @@ struct TileLoader {
     static constexpr int LDS_STRIDE = BK + 16 / sizeof(S);  // elements per LDS row
     // K-major: R * BK / V vectors; MN-major: (R / V) * (BK / 4) units of 4 vectors.
     static constexpr int kLoads = 4;
-    static_assert((KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) == kLoads * kThreads,
+    static_assert((KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) == kLoads * THREADS,
                   "tile shape and thread count disagree");
     uint4 reg[kLoads];
 
@@ -101,7 +102,7 @@ struct TileLoader {
         if constexpr (KMAJOR) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) {
-                const int v = tid + i * kThreads;
+                const int v = tid + i * THREADS;
                 const int r = v / (BK / V), kc = v % (BK / V);
                 const int64_t gr = r0 + r, gk = k0 + kc * V;
                 if (gr < rows && gk < K) {
@@ -130,7 +131,7 @@ struct TileLoader {
         if constexpr (KMAJOR) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) {
-                const int v = tid + i * kThreads;
+                const int v = tid + i * THREADS;
                 const int r = v / (BK / V), kc = v % (BK / V);
                 *reinterpret_cast<uint4*>(lds + r * LDS_STRIDE + kc * V) = reg[i];
             }
@@ -179,25 +180,28 @@ __device__ __forceinline__ void tile_coords(int bid, int grid_m, int grid_n, int
     pn = (pid % in_group) / size_m;
 }
 
-template <typename T, bool A_KMAJOR, bool B_KMAJOR>
-__global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
+template <typename T, bool A_KMAJOR, bool B_KMAJOR, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) {
     using S = typename Elem<T>::storage;
-    using LA = TileLoader<T, kBM, A_KMAJOR>;
-    using LB = TileLoader<T, kBN, B_KMAJOR>;
+    constexpr int THREADS = WM * WN * kWave;
+    using LA = TileLoader<T, BM, A_KMAJOR, THREADS>;
+    using LB = TileLoader<T, BN, B_KMAJOR, THREADS>;
     constexpr int BK = Mfma<T>::BK, KSUB = Mfma<T>::KSUB;
     constexpr int LDS_STRIDE = LA::LDS_STRIDE;
+    constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
     constexpr int TM = kWaveM / 32, TN = kWaveN / 32;
-    __shared__ __attribute__((aligned(16))) S As[kBM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) S Bs[kBN * LDS_STRIDE];
+    constexpr int STAGE = (BM + BN) * LDS_STRIDE;  // elements per LDS stage
+    __shared__ __attribute__((aligned(16))) S lds[2 * STAGE];
 
-    const int grid_m = static_cast<int>((p.m + kBM - 1) / kBM);
-    const int grid_n = static_cast<int>((p.n + kBN - 1) / kBN);
+    const int grid_m = static_cast<int>((p.m + BM - 1) / BM);
+    const int grid_n = static_cast<int>((p.n + BN - 1) / BN);
     int pm, pn;
     tile_coords(blockIdx.x, grid_m, grid_n, pm, pn);
-    const int64_t m0 = static_cast<int64_t>(pm) * kBM, n0 = static_cast<int64_t>(pn) * kBN;
+    const int64_t m0 = static_cast<int64_t>(pm) * BM, n0 = static_cast<int64_t>(pn) * BN;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WN, wn = wave % WN;
     const int half = lane / 32, l32 = lane % 32;
+    const int64_t nk = (p.k + BK - 1) / BK;
 
     for (int64_t bi = blockIdx.z; bi < p.batch; bi += gridDim.z) {
         const S* A = static_cast<const S*>(p.a) + bi * p.stride_a;
@@ -212,17 +216,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
 
         LA la;
         LB lb;
+        // Prologue: K tile 0 into stage 0, K tile 1 in flight.
         la.load(A, p.lda, m0, p.m, 0, p.k);
         lb.load(B, p.ldb, n0, p.n, 0, p.k);
-        for (int64_t k0 = 0; k0 < p.k; k0 += BK) {
-            la.store(As);
-            lb.store(Bs);
-            __syncthreads();
-            if (k0 + BK < p.k) {
-                la.load(A, p.lda, m0, p.m, k0 + BK, p.k);
-                lb.load(B, p.ldb, n0, p.n, k0 + BK, p.k);
-            }
-#pragma unroll
+        la.store(lds);
+        lb.store(lds + BM * LDS_STRIDE);
+        if (nk > 1) {
+            la.load(A, p.lda, m0, p.m, BK, p.k);
+            lb.load(B, p.ldb, n0, p.n, BK, p.k);
+        }
+        __syncthreads();
+        for (int64_t kt = 0; kt < nk; ++kt) {
+            const S* As = lds + (kt & 1) * STAGE;
+            const S* Bs = As + BM * LDS_STRIDE;
+#pragma unroll 2
             for (int s = 0; s < BK / KSUB; ++s) {
                 uint4 af[TM], bf[TN];
 #pragma unroll
@@ -241,6 +248,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[i], bf[j], acc[i][j]);
+            }
+            // The other stage was last read in step kt - 1, before the
+            // barrier that ended it: fill it with K tile kt + 1 and start
+            // loading tile kt + 2.
+            if (kt + 1 < nk) {
+                S* next = lds + ((kt + 1) & 1) * STAGE;
+                la.store(next);
+                lb.store(next + BM * LDS_STRIDE);
+            }
+            if (kt + 2 < nk) {
+                la.load(A, p.lda, m0, p.m, (kt + 2) * BK, p.k);
+                lb.load(B, p.ldb, n0, p.n, (kt + 2) * BK, p.k);
             }
             __syncthreads();
         }
@@ -297,20 +316,41 @@ bool mfma_eligible(const GemmArgs& p) {
     };
     return p.k > 0 && ok(p.a, p.lda, p.stride_a, a_kmajor, p.m) &&
            ok(p.b, p.ldb, p.stride_b, b_kmajor, p.n) &&
-           (p.m + kBM - 1) / kBM * ((p.n + kBN - 1) / kBN) < (int64_t(1) << 31);
+           (p.m + 127) / 128 * ((p.n + 127) / 128) < (int64_t(1) << 31);
 }
 
-template <typename T>
-void launch_mfma(const GemmArgs& p, hipStream_t stream) {
-    const int64_t tiles = ((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
+template <typename T, int BM, int BN, int WM, int WN>
+void launch_config(const GemmArgs& p, hipStream_t stream) {
+    constexpr int THREADS = WM * WN * kWave;
+    const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
     const dim3 grid(static_cast<unsigned>(tiles), 1u,
                     static_cast<unsigned>(p.batch < 65535 ? p.batch : 65535));
     const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
-    if (a_kmajor && b_kmajor) gemm_mfma_kernel<T, true, true><<<grid, kThreads, 0, stream>>>(p);
-    else if (a_kmajor) gemm_mfma_kernel<T, true, false><<<grid, kThreads, 0, stream>>>(p);
-    else if (b_kmajor) gemm_mfma_kernel<T, false, true><<<grid, kThreads, 0, stream>>>(p);
-    else gemm_mfma_kernel<T, false, false><<<grid, kThreads, 0, stream>>>(p);
+    if (a_kmajor && b_kmajor) {
+        gemm_mfma_kernel<T, true, true, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+    } else if (a_kmajor) {
+        gemm_mfma_kernel<T, true, false, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+    } else if (b_kmajor) {
+        gemm_mfma_kernel<T, false, true, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+    } else {
+        gemm_mfma_kernel<T, false, false, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+    }
     TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+// 16-bit types take the big tile when it still gives every CU a block;
+// float32 (bound by its much slower MFMA rate) keeps the small one, whose
+// registers fit without spilling.
+template <typename T>
+void launch_mfma(const GemmArgs& p, hipStream_t stream) {
+    int device = 0;
+    TP_AMD_HIP_CHECK(hipGetDevice(&device));
+    const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
+    if (sizeof(typename Elem<T>::storage) == 2 && big_tiles >= cu_count(device)) {
+        launch_config<T, 256, 256, 2, 4>(p, stream);
+    } else {
+        launch_config<T, 128, 128, 2, 2>(p, stream);
+    }
 }
 
 template <typename T>
