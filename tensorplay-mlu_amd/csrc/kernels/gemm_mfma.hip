@@ -82,6 +82,10 @@ struct Mfma<float> {
 
 constexpr int kGroupM = 8;
 
+__device__ __forceinline__ uint32_t component(const uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 // One operand's tile loader: R rows (M or N) x BK, into LDS [R][BK + pad].
 // KMAJOR: element (r, k) at X[r * ld + k]; otherwise at X[k * ld + r].
 template <typename T, int R, bool KMAJOR, int THREADS>
@@ -90,9 +94,12 @@ struct TileLoader {
     static constexpr int V = Mfma<T>::V;
     static constexpr int BK = Mfma<T>::BK;
     static constexpr int LDS_STRIDE = BK + 16 / sizeof(S);  // elements per LDS row
-    // K-major: R * BK / V vectors; MN-major: (R / V) * (BK / 4) units of 4 vectors.
-    static constexpr int kLoads = 4;
-    static_assert((KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) == kLoads * THREADS,
+    // K-major: R * BK / V vectors; MN-major: (R / V) * (BK / 4) units of 4
+    // vectors (V along M/N by 4 along K).
+    static constexpr int kLoads = (KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) / THREADS;
+    static constexpr int kUnits = kLoads / 4;  // MN-major units per thread
+    static_assert(kLoads * THREADS == (KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) &&
+                      (KMAJOR || kUnits * 4 == kLoads),
                   "tile shape and thread count disagree");
     uint4 reg[kLoads];
 
@@ -112,15 +119,19 @@ struct TileLoader {
                 }
             }
         } else {
-            const int rb = tid % (R / V), kb = tid / (R / V);
-            const int64_t gr = r0 + rb * V;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t gk = k0 + kb * 4 + i;
-                if (gr < rows && gk < K) {
-                    reg[i] = *reinterpret_cast<const uint4*>(X + gk * ld + gr);
-                } else {
-                    reg[i] = make_uint4(0, 0, 0, 0);
+            for (int u = 0; u < kUnits; ++u) {
+                const int unit = tid + u * THREADS;
+                const int kb = unit % (BK / 4), rb = unit / (BK / 4);
+                const int64_t gr = r0 + rb * V;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t gk = k0 + kb * 4 + i;
+                    if (gr < rows && gk < K) {
+                        reg[u * 4 + i] = *reinterpret_cast<const uint4*>(X + gk * ld + gr);
+                    } else {
+                        reg[u * 4 + i] = make_uint4(0, 0, 0, 0);
+                    }
                 }
             }
         }
@@ -136,29 +147,38 @@ struct TileLoader {
                 *reinterpret_cast<uint4*>(lds + r * LDS_STRIDE + kc * V) = reg[i];
             }
         } else {
-            const int rb = tid % (R / V), kb = tid / (R / V);
-            if constexpr (sizeof(S) == 4) {
-                // 4 (k) x 4 (r) floats -> 4 rows of 4 consecutive k.
-                const uint32_t* in = reinterpret_cast<const uint32_t*>(reg);
+            // Consecutive lanes take consecutive K blocks of one M/N block, so
+            // the rows they write lie side by side in the LDS banks (with the
+            // M/N block varying fastest, 32 lanes would land on two banks).
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint4 out = make_uint4(in[0 * 4 + j], in[1 * 4 + j], in[2 * 4 + j],
-                                                 in[3 * 4 + j]);
-                    *reinterpret_cast<uint4*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
-                }
-            } else {
-                // 4 (k) x 8 (r) 16-bit values -> 8 rows of 4 consecutive k.
-                const uint32_t* in = reinterpret_cast<const uint32_t*>(reg);
+            for (int u = 0; u < kUnits; ++u) {
+                const int unit = tid + u * THREADS;
+                const int kb = unit % (BK / 4), rb = unit / (BK / 4);
+                const uint4* in = reg + u * 4;
+                if constexpr (sizeof(S) == 4) {
+                    // 4 (k) x 4 (r) floats -> 4 rows of 4 consecutive k.
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int p = j / 2, hi = j % 2;
-                    uint32_t w[4];
+                    for (int j = 0; j < 4; ++j) {
+                        const uint4 out = make_uint4(component(in[0], j), component(in[1], j),
+                                                     component(in[2], j), component(in[3], j));
+                        *reinterpret_cast<uint4*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
+                    }
+                } else {
+                    // 4 (k) x 8 (r) 16-bit values -> 8 rows of 4 consecutive k.
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) w[i] = hi ? (in[i * 4 + p] >> 16) : (in[i * 4 + p] & 0xffffu);
-                    uint2 out;
-                    out.x = w[0] | (w[1] << 16);
-                    out.y = w[2] | (w[3] << 16);
-                    *reinterpret_cast<uint2*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
+                    for (int j = 0; j < 8; ++j) {
+                        const int p = j / 2, hi = j % 2;
+                        uint32_t w[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint32_t c = component(in[i], p);
+                            w[i] = hi ? (c >> 16) : (c & 0xffffu);
+                        }
+                        uint2 out;
+                        out.x = w[0] | (w[1] << 16);
+                        out.y = w[2] | (w[3] << 16);
+                        *reinterpret_cast<uint2*>(lds + (rb * V + j) * LDS_STRIDE + kb * 4) = out;
+                    }
                 }
             }
         }
@@ -345,12 +365,14 @@ template <typename T>
 void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
-    const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
-    if (sizeof(typename Elem<T>::storage) == 2 && big_tiles >= cu_count(device)) {
-        launch_config<T, 256, 256, 2, 4>(p, stream);
-    } else {
-        launch_config<T, 128, 128, 2, 2>(p, stream);
+    if constexpr (sizeof(typename Elem<T>::storage) == 2) {
+        const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
+        if (big_tiles >= cu_count(device)) {
+            launch_config<T, 256, 256, 2, 4>(p, stream);
+            return;
+        }
     }
+    launch_config<T, 128, 128, 2, 2>(p, stream);
 }
 
 template <typename T>
