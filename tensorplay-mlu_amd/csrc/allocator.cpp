@@ -59,6 +59,10 @@ void empty_cache() { instance().empty_cache(device_count()); }
 
 using namespace tp_amd;
 
+// Defined by the TensorPlay adapter when it is linked in (csrc/tensorplay/,
+// make TENSORPLAY_INCLUDE=...); null otherwise.
+extern "C" int tp_amd_tensorplay_register(void) __attribute__((weak));
+
 extern "C" {
 
 void tp_mlu_memory_stats(int index, int64_t* out) {
@@ -107,7 +111,12 @@ int tp_mlu_init(void) {
         // first operator does not pay for it.
         for (int d = 0; d < device_count(); ++d) (void)stream(d);
     });
-    return status == TP_AMD_OK ? 0 : 1;
+    if (status != TP_AMD_OK) return 1;
+    // Built with the TensorPlay adapter (csrc/tensorplay/), the operators
+    // without a device kernel are routed to TensorPlay's host kernels here,
+    // as the reference's tp_mlu_init does (Module.cpp:15-22).
+    if (tp_amd_tensorplay_register != nullptr && tp_amd_tensorplay_register() != 0) return 1;
+    return 0;
 }
 
 }  // extern "C"
