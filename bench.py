@@ -237,6 +237,35 @@ def suite_gemm(ops, dev, ev):
     return out
 
 
+def suite_config5b(ops, dev, ev):
+    """Config 5b: the fp32 MLP training step at full size (batch 8192, four
+    Linear(4096, 4096) + ReLU layers, Linear(4096, 1000), log_softmax, NLL via
+    mul + sum, backward, SGD), every operator through the C-ABI; TFLOP/s of
+    the step's GEMM work against the fp32 MFMA peak."""
+    wl = importlib.import_module("tensorplay-mlu_amd.workloads")
+    batch, width, layers, classes = 8192, 4096, 4, 1000
+    ws, bs = wl.MLP.host_init(width, layers, width, classes, seed=0)
+    model = wl.MLP.to_device(ws, bs)
+    del ws, bs
+    g = np.random.default_rng(100)
+    x = dev.from_numpy(g.standard_normal((batch, width), dtype=np.float32))
+    labels = np.random.default_rng(101).integers(0, classes, batch)
+    onehot = np.zeros((batch, classes), np.float32)
+    onehot[np.arange(batch), labels] = 1.0
+    onehot = dev.from_numpy(onehot)
+
+    def step():
+        wl.mlp_step(ops, model, x, onehot, 1e-3)
+
+    step()
+    ms = ev.time_ms(step, 3)
+    flops = wl.mlp_step_flops(batch, width, layers, classes)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"mlp_step_fp32": {"ms": round(ms, 2), "TFLOP/s": round(tf, 1),
+                              "mfma_frac": round(tf / MFMA_PEAK_TFLOPS["fp32"], 4),
+                              "flops_per_step": flops}}
+
+
 def cpu_baseline(rows: int = 1024):
     """The C oracle (CPU port, float64 arithmetic, OpenMP) on the first
     ``rows`` rows of config 2, both dtypes; GB/s of algorithmic bytes."""
@@ -348,6 +377,8 @@ def main() -> int:
         suite["config3"] = suite_config3(ops, dev, ev)
         log("bench: suite configs 4 and 5a")
         suite["config4_5a"] = suite_gemm(ops, dev, ev)
+        log("bench: suite config 5b")
+        suite["config5b"] = suite_config5b(ops, dev, ev)
         result["suite"] = suite
     if not args.no_cpu:
         log("bench: cpu baseline")
