@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace tp_amd {
 
@@ -23,11 +24,18 @@ __device__ __forceinline__ float bf16_to_float(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
+// Round to nearest even, NaN kept quiet (sign and the payload's high bits
+// kept, quiet bit set): v_cvt_pk_bf16_f32, which gives exactly these bits
+// for every float32 input -- the same as the integer form
+// u + 0x7fff + ((u >> 16) & 1) for non-NaN u, (u >> 16) | 0x40 for NaN.
 __device__ __forceinline__ uint16_t float_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float floatx2 __attribute__((ext_vector_type(2)));
+    const floatx2 v = {f, 0.0f};
+    const bf16x2 b = __builtin_convertvector(v, bf16x2);
+    uint32_t u;
+    __builtin_memcpy(&u, &b, 4);
+    return static_cast<uint16_t>(u & 0xffffu);
 }
 
 __device__ __forceinline__ float f16_to_float(uint16_t h) {
@@ -109,6 +117,70 @@ __device__ __forceinline__ void store_packet_nt(typename Elem<T>::storage* p, co
     uint4 raw;
     __builtin_memcpy(&raw, &v, 16);
     uint4* q = reinterpret_cast<uint4*>(p);
+    __builtin_nontemporal_store(raw.x, &q->x);
+    __builtin_nontemporal_store(raw.y, &q->y);
+    __builtin_nontemporal_store(raw.z, &q->z);
+    __builtin_nontemporal_store(raw.w, &q->w);
+}
+
+// Raw 16-byte packets converted to and from float32 lanes, for kernels whose
+// per-element arithmetic is the limit (softmax, transcendental activations):
+// bfloat16 unpacks with one shift or mask per element and packs two elements
+// per v_cvt_pk_bf16_f32 (round to nearest even, as float_to_bf16 for every
+// non-NaN input); float16 converts with v_cvt_f16_f32 (round to nearest even).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ void unpack(const uint4& raw, float (&f)[Packet<T>::N]) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(typename Elem<T>::storage) == 4) {
+            f[i] = __uint_as_float(w[i]);
+        } else if constexpr (std::is_same_v<T, bf16_t>) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        } else {
+            f[2 * i] = f16_to_float(static_cast<uint16_t>(w[i] & 0xffffu));
+            f[2 * i + 1] = f16_to_float(static_cast<uint16_t>(w[i] >> 16));
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack(const float (&f)[Packet<T>::N]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(typename Elem<T>::storage) == 4) {
+            w[i] = __float_as_uint(f[i]);
+        } else if constexpr (std::is_same_v<T, bf16_t>) {
+            const floatx2_t v = {f[2 * i], f[2 * i + 1]};
+            const bf16x2_t b = __builtin_convertvector(v, bf16x2_t);
+            __builtin_memcpy(&w[i], &b, 4);
+        } else {
+            const floatx2_t v = {f[2 * i], f[2 * i + 1]};
+            const f16x2_t h = __builtin_convertvector(v, f16x2_t);
+            __builtin_memcpy(&w[i], &h, 4);
+        }
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ uint4 load_raw_nt(const void* p) {
+    const uint4* q = static_cast<const uint4*>(p);
+    uint4 raw;
+    raw.x = __builtin_nontemporal_load(&q->x);
+    raw.y = __builtin_nontemporal_load(&q->y);
+    raw.z = __builtin_nontemporal_load(&q->z);
+    raw.w = __builtin_nontemporal_load(&q->w);
+    return raw;
+}
+
+__device__ __forceinline__ void store_raw_nt(void* p, const uint4& raw) {
+    uint4* q = static_cast<uint4*>(p);
     __builtin_nontemporal_store(raw.x, &q->x);
     __builtin_nontemporal_store(raw.y, &q->y);
     __builtin_nontemporal_store(raw.z, &q->z);

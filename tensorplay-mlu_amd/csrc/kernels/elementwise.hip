@@ -23,6 +23,10 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;
 
+// 16-bit storage takes the fast transcendental forms (math_ops.h).
+template <typename T>
+constexpr bool kFast = sizeof(typename Elem<T>::storage) == 2;
+
 #define TP_AMD_DISPATCH_FLOAT(dtype, T, ...)                                      \
     switch (dtype) {                                                              \
         case TP_AMD_FLOAT32: { using T = float; __VA_ARGS__; break; }             \
@@ -54,15 +58,13 @@ __global__ __launch_bounds__(kBlock) void flat_kernel(const typename Elem<T>::st
     for (int k = 0; k < kUnroll; ++k) {
         const int64_t p = base + k * kBlock;
         if (p < npackets) {
-            Packet<T> y;
+            float y[N];
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                float v;
-                if constexpr (NIN == 1) v = f(Elem<T>::load(x0[k].v[j]));
-                else v = f(Elem<T>::load(x0[k].v[j]), Elem<T>::load(x1[k].v[j]));
-                y.v[j] = Elem<T>::store(v);
+                if constexpr (NIN == 1) y[j] = f(Elem<T>::load(x0[k].v[j]));
+                else y[j] = f(Elem<T>::load(x0[k].v[j]), Elem<T>::load(x1[k].v[j]));
             }
-            store_packet_nt<T>(out + p * N, y);
+            store_raw_nt(out + p * N, pack<T>(y));
         }
     }
     // The n % N trailing elements, one per thread of block 0.
@@ -128,12 +130,12 @@ __global__ __launch_bounds__(kBlock) void binary2d_kernel(const typename Elem<T>
     for (int k = 0; k < kUnroll; ++k) {
         const int64_t p = base + k * kBlock;
         if (p < npackets) {
-            Packet<T> y;
+            float y[N];
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                y.v[j] = Elem<T>::store(f(Elem<T>::load(xa[k].v[j]), Elem<T>::load(xb[k].v[j])));
+                y[j] = f(Elem<T>::load(xa[k].v[j]), Elem<T>::load(xb[k].v[j]));
             }
-            store_packet_nt<T>(out + p * N, y);
+            store_raw_nt(out + p * N, pack<T>(y));
         }
     }
 }
@@ -309,7 +311,7 @@ void unary_typed(int device, int ndim, const int64_t* sizes, const void* x, cons
 
 #define TP_AMD_UNARY_CASE(OP)                                                         \
     case OP:                                                                          \
-        unary_typed<T>(index, ndim, sizes, x, x_strides, y, UnaryFn<OP>{param});      \
+        unary_typed<T>(index, ndim, sizes, x, x_strides, y, UnaryFn<OP, kFast<T>>{param}); \
         break;
 
 template <typename T>
@@ -337,7 +339,7 @@ void unary_dispatch(int index, int op, int ndim, const int64_t* sizes, const voi
 
 #define TP_AMD_BWD_CASE(OP)                                                            \
     case OP:                                                                           \
-        launch_flat<T, 2>(index, grad, saved, dx, n, BackwardFn<OP>{param});           \
+        launch_flat<T, 2>(index, grad, saved, dx, n, BackwardFn<OP, kFast<T>>{param}); \
         break;
 
 template <typename T>

@@ -16,6 +16,9 @@
 
 #include <cmath>
 
+#include <climits>
+#include <cstdint>
+
 #include "device_common.h"
 #include "../allocator.h"
 #include "../runtime.h"
@@ -67,6 +70,60 @@ __device__ __forceinline__ float wave_reduce(float v) {
     return v;
 }
 
+// ---- amax / amin on order-preserving integer keys -------------------------------
+//
+// Flipping the magnitude bits of negative values maps the float order
+// (with -0 below +0) onto the signed integer order: key(u) = u ^ ((u >> 31) &
+// 0x7fff...), an involution.  NaNs map beyond +-inf, so an integer max / min
+// gives the exact amax / amin unless a NaN wins; a thread whose result comes
+// out NaN (a NaN among its elements, or no elements) recomputes its elements
+// with the NaN-skipping float combine.  For 16-bit storage two keys share a
+// register and one packed v_pk_max_i16 / v_pk_min_i16 covers both.
+template <int OP>
+constexpr bool kMinMax = OP == TP_AMD_REDUCE_AMAX || OP == TP_AMD_REDUCE_AMIN;
+
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int32_t key32(uint32_t u) {
+    return static_cast<int32_t>(u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) &
+                                     0x7fffffffu));
+}
+__device__ __forceinline__ short2_t key16x2(uint32_t w) {
+    short2_t h;
+    __builtin_memcpy(&h, &w, 4);
+    const short2_t m = (h >> static_cast<short>(15)) & static_cast<short>(0x7fff);
+    return h ^ m;
+}
+
+template <int OP>
+struct KeyOps {
+    static constexpr bool kMax = OP == TP_AMD_REDUCE_AMAX;
+    // The identity is the key no value beats; it decodes to a NaN, so an
+    // empty thread falls back to the float combine (which returns NaN too).
+    __device__ __forceinline__ static int32_t id32() { return kMax ? INT32_MIN : INT32_MAX; }
+    __device__ __forceinline__ static short id16() {
+        return kMax ? static_cast<short>(-32768) : static_cast<short>(32767);
+    }
+    __device__ __forceinline__ static int32_t pick(int32_t a, int32_t b) {
+        return kMax ? (a > b ? a : b) : (a < b ? a : b);
+    }
+    __device__ __forceinline__ static short2_t pick(short2_t a, short2_t b) {
+        return kMax ? __builtin_elementwise_max(a, b) : __builtin_elementwise_min(a, b);
+    }
+    // Float value of a 32-bit key.
+    __device__ __forceinline__ static float value32(int32_t k) {
+        const uint32_t u = static_cast<uint32_t>(k);
+        return __uint_as_float(u ^ (static_cast<uint32_t>(k >> 31) & 0x7fffffffu));
+    }
+    // Float value of the better of a pair of 16-bit keys.
+    template <typename Tin>
+    __device__ __forceinline__ static float value16(short2_t k) {
+        const short b = kMax ? (k.x > k.y ? k.x : k.y) : (k.x < k.y ? k.x : k.y);
+        const uint16_t u = static_cast<uint16_t>(b) ^ (b < 0 ? 0x7fffu : 0u);
+        return Elem<Tin>::load(u);
+    }
+};
+
 // Final value of a reduction: the mean divides the float32 sum by the
 // number of reduced elements.
 template <int OP>
@@ -75,6 +132,64 @@ __device__ __forceinline__ float finish(float v, int64_t count, bool final_pass)
         if (final_pass) return v / static_cast<float>(count);
     }
     return v;
+}
+
+// One thread's share of packets [pb, pe) of a row segment: packets
+// pb + tid, pb + tid + THREADS, ...  Float combine in element order.
+template <typename Tin, int OP, int THREADS>
+__device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p, int64_t pb,
+                                           int64_t pe, int tid) {
+    constexpr int N = Packet<Tin>::N;
+    constexpr int U = 4;
+    float acc = Combine<OP>::identity();
+    int64_t q = pb + tid;
+    for (; q + (U - 1) * THREADS < pe; q += U * THREADS) {
+        Packet<Tin> v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = load_packet_nt<Tin>(p + (q + u * THREADS) * N);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v[u].v[j]));
+    }
+    for (; q < pe; q += THREADS) {
+        const Packet<Tin> v = load_packet_nt<Tin>(p + q * N);
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v.v[j]));
+    }
+    return acc;
+}
+
+// The same share for amax / amin on integer keys (NaN when a NaN wins or the
+// share is empty).
+template <typename Tin, int OP, int THREADS>
+__device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, int64_t pb,
+                                          int64_t pe, int tid) {
+    constexpr int N = Packet<Tin>::N;
+    constexpr int U = 4;
+    using K = KeyOps<OP>;
+    constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
+    int32_t k32 = K::id32();
+    short2_t k16 = {K::id16(), K::id16()};
+    auto take = [&](const uint4& raw) {
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (kWide) k32 = K::pick(k32, key32(w[i]));
+            else k16 = K::pick(k16, key16x2(w[i]));
+        }
+    };
+    int64_t q = pb + tid;
+    for (; q + (U - 1) * THREADS < pe; q += U * THREADS) {
+        uint4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = load_raw_nt(p + (q + u * THREADS) * N);
+#pragma unroll
+        for (int u = 0; u < U; ++u) take(raw[u]);
+    }
+    for (; q < pe; q += THREADS) take(load_raw_nt(p + q * N));
+    if constexpr (kWide) return K::value32(k32);
+    else return K::template value16<Tin>(k16);
 }
 
 // Row segments.  Segment s covers row s / nseg, elements
@@ -99,22 +214,11 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
         if constexpr (VEC) {
             // begin and end are multiples of N (chunk and r are).
             const int64_t pb = begin / N, pe = end / N;
-            constexpr int U = 4;
-            int64_t q = pb + tid;
-            for (; q + (U - 1) * kThreads < pe; q += U * kThreads) {
-                Packet<Tin> v[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) v[u] = load_packet_nt<Tin>(p + (q + u * kThreads) * N);
-#pragma unroll
-                for (int u = 0; u < U; ++u)
-#pragma unroll
-                    for (int j = 0; j < N; ++j)
-                        acc = Combine<OP>::apply(acc, Elem<Tin>::load(v[u].v[j]));
-            }
-            for (; q < pe; q += kThreads) {
-                const Packet<Tin> v = load_packet_nt<Tin>(p + q * N);
-#pragma unroll
-                for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v.v[j]));
+            if constexpr (kMinMax<OP>) {
+                acc = row_keys<Tin, OP, kThreads>(p, pb, pe, tid);
+                if (acc != acc) acc = row_exact<Tin, OP, kThreads>(p, pb, pe, tid);
+            } else {
+                acc = row_exact<Tin, OP, kThreads>(p, pb, pe, tid);
             }
         } else {
             for (int64_t j = begin + tid; j < end; j += kThreads) {
@@ -139,6 +243,51 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
     }
 }
 
+// amax / amin of one thread's N columns over rows row0, row0 + 4, ... < end
+// on integer keys (a column comes out NaN when a NaN wins or it has no rows).
+template <typename Tin, int OP>
+__device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
+                                          const typename Elem<Tin>::storage* p, int64_t row0,
+                                          int64_t end, int64_t inner) {
+    constexpr int G = kBlock / 64;  // row groups
+    constexpr int U = 4;
+    using K = KeyOps<OP>;
+    constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
+    int32_t k32[4];
+    short2_t k16[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        k32[i] = K::id32();
+        k16[i] = short2_t{K::id16(), K::id16()};
+    }
+    auto take = [&](const uint4& raw) {
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (kWide) k32[i] = K::pick(k32[i], key32(w[i]));
+            else k16[i] = K::pick(k16[i], key16x2(w[i]));
+        }
+    };
+    int64_t row = row0;
+    for (; row + (U - 1) * G < end; row += U * G) {
+        uint4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = load_raw_nt(p + (row + u * G) * inner);
+#pragma unroll
+        for (int u = 0; u < U; ++u) take(raw[u]);
+    }
+    for (; row < end; row += G) take(load_raw_nt(p + row * inner));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (kWide) {
+            acc[i] = K::value32(k32[i]);
+        } else {
+            acc[2 * i] = K::template value16<Tin>(short2_t{k16[i].x, k16[i].x});
+            acc[2 * i + 1] = K::template value16<Tin>(short2_t{k16[i].y, k16[i].y});
+        }
+    }
+}
+
 // Column chunks.  Block (bx, ch, z): columns [bx * 64 * N, +64 * N) of every
 // outer index o = z, z + gridDim.z, ...; rows [ch * chunk, +chunk) split
 // over 4 row groups.  Writes out[(o * nchunk + ch) * inner + col].
@@ -160,7 +309,19 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
         float acc[N];
 #pragma unroll
         for (int j = 0; j < N; ++j) acc[j] = Combine<OP>::identity();
-        if (col < inner) {
+        bool exact = !(kMinMax<OP> && VEC);
+        if constexpr (kMinMax<OP> && VEC) {
+            if (col < inner) {
+                cols_keys<Tin, OP>(acc, x + o * r * inner + col, begin + rg, end, inner);
+#pragma unroll
+                for (int j = 0; j < N; ++j) exact = exact || acc[j] != acc[j];
+                if (exact) {
+#pragma unroll
+                    for (int j = 0; j < N; ++j) acc[j] = Combine<OP>::identity();
+                }
+            }
+        }
+        if (exact && col < inner) {
             const typename Elem<Tin>::storage* p = x + o * r * inner + col;
             int64_t row = begin + rg;
             constexpr int U = 4;

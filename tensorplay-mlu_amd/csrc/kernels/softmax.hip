@@ -3,15 +3,23 @@
 // tensorplay_mlu/csrc/ReduceKernels.cpp:171-199).
 //
 // Rows along the last axis (inner == 1) are held in registers: each row is
-// read from HBM once and written once.  WAVES wavefronts share a row and
-// each thread keeps VPT 16-byte packets of it, so rows up to
-// 64 * WAVES * VPT * N elements (65536 fp32 forward, 32768 fp32 backward)
-// stay on chip; the row max and the exponential sum combine across lanes
-// with shuffles and across waves in LDS.  Rows too long for that, or whose
-// length is not a multiple of the packet, take a block-per-row kernel that
-// keeps a running (max, sum) pair and reads the row twice.  Softmax over a
-// leading axis (inner > 1) walks the reduced axis with the contiguous inner
-// axis across threads.
+// read from HBM once and written once.  A configuration (WAVES, EPT) gives a
+// row WAVES wavefronts and each thread EPT elements (EPT / N 16-byte
+// packets), so rows up to 64 * WAVES * EPT elements stay on chip; up to 4
+// waves per row, a 256-thread block holds 4 / WAVES rows, so several blocks
+// share a CU.  The row max and the exponential sum combine across lanes with
+// shuffles and across waves in LDS.  Longer rows (a multiple of the packet,
+// 16-byte aligned) take a block-per-row kernel that keeps a running (max,
+// sum) per thread over the row, then re-reads it -- from L2, which holds the
+// CU's current row -- to write the result.  Anything else takes a scalar
+// block-per-row kernel.  Softmax over a leading axis (inner > 1) walks the
+// reduced axis with the contiguous inner axis across threads.
+//
+// The per-element arithmetic is kept short because for 16-bit storage it,
+// not HBM, would set the pace: exponentials are 2^(d log2 e) on v_exp_f32
+// with d = x - max formed first, the softmax quotient is one reciprocal per
+// row, and results are packed with the hardware round-to-nearest-even
+// conversions.
 
 #include <cmath>
 
@@ -24,6 +32,11 @@ namespace tp_amd {
 namespace {
 
 constexpr int kBlock = 256;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// e^d on v_exp_f32 (the softmax arguments d = x - max are <= 0, where its
+// error stays within a few float32 ulps).
+__device__ __forceinline__ float exp_fast(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -36,39 +49,46 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Reduce ``v`` over the WAVES waves that share a row (WAVES > 1: the whole
-// block is one row).  ``scratch`` holds one float per wave.
+// Layout of a (WAVES, EPT) configuration: WAVES <= 4 packs 4 / WAVES rows
+// into a 256-thread block; more waves make one row per block.
+template <int WAVES>
+constexpr int block_threads() {
+    return WAVES >= 4 ? WAVES * kWave : kBlock;
+}
+template <int WAVES>
+constexpr int rows_per_block() {
+    return WAVES >= 4 ? 1 : 4 / WAVES;
+}
+
+// Reduce ``v`` over the WAVES waves of this thread's row.  ``scratch`` holds
+// one float per wave of the block.  Every wave of the block must call it.
 template <int WAVES, bool MAX>
 __device__ __forceinline__ float row_reduce(float v, float* scratch) {
     v = MAX ? wave_max(v) : wave_sum(v);
     if constexpr (WAVES > 1) {
         const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+        const int first = (wave / WAVES) * WAVES;
         __syncthreads();  // scratch may still be read from the previous use
         if (lane == 0) scratch[wave] = v;
         __syncthreads();
-        float t = lane < WAVES ? scratch[lane] : (MAX ? -INFINITY : 0.0f);
+        const float t = lane < WAVES ? scratch[first + lane] : (MAX ? -INFINITY : 0.0f);
         v = MAX ? wave_max(t) : wave_sum(t);
     }
     return v;
 }
 
-// Block size for a config: one wave per row packs 4 rows into 256 threads.
-template <int WAVES>
-constexpr int block_threads() {
-    return WAVES == 1 ? kBlock : WAVES * kWave;
-}
-
-template <typename T, int WAVES, int VPT>
+template <typename T, int WAVES, int EPT>
 __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_rows_kernel(
     const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t rows, int64_t D,
     bool log) {
     constexpr int N = Packet<T>::N;
-    constexpr int kRowsPerBlock = WAVES == 1 ? kBlock / kWave : 1;
+    constexpr int VPT = EPT / N;
+    static_assert(VPT * N == EPT, "EPT must be a whole number of packets");
     constexpr int kThreads = WAVES * kWave;
-    __shared__ float scratch[WAVES > 1 ? WAVES : 1];
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock +
-                        (WAVES == 1 ? threadIdx.x / kWave : 0);
-    const int tid = WAVES == 1 ? threadIdx.x % kWave : threadIdx.x;
+    __shared__ float scratch[block_threads<WAVES>() / kWave];
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block<WAVES>() +
+                        threadIdx.x / kThreads;
+    const int tid = threadIdx.x % kThreads;
     const bool active = row < rows;  // uniform per wave
     const int64_t npk = D / N;
     const typename Elem<T>::storage* xr = x + (active ? row : 0) * D;
@@ -78,12 +98,9 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_rows_kernel(
     for (int k = 0; k < VPT; ++k) {
         const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
         if (active && q < npk) {
-            const Packet<T> p = load_packet_nt<T>(xr + q * N);
+            unpack<T>(load_raw_nt(xr + q * N), v[k]);
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                v[k][j] = Elem<T>::load(p.v[j]);
-                m = fmaxf(m, v[k][j]);
-            }
+            for (int j = 0; j < N; ++j) m = fmaxf(m, v[k][j]);
         } else {
 #pragma unroll
             for (int j = 0; j < N; ++j) v[k][j] = -INFINITY;
@@ -98,57 +115,64 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_rows_kernel(
     for (int k = 0; k < VPT; ++k)
 #pragma unroll
         for (int j = 0; j < N; ++j) {
-            v[k][j] = log ? v[k][j] - shift : expf(v[k][j] - shift);
-            s += log ? expf(v[k][j]) : v[k][j];
+            v[k][j] -= shift;
+            const float e = exp_fast(v[k][j]);
+            s += e;
+            if (!log) v[k][j] = e;
         }
     s = row_reduce<WAVES, false>(s, scratch);
-    const float lse = logf(s);
     if (!active) return;
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
     typename Elem<T>::storage* yr = y + row * D;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
         if (q < npk) {
-            Packet<T> p;
+            float o[N];
 #pragma unroll
-            for (int j = 0; j < N; ++j) p.v[j] = Elem<T>::store(log ? v[k][j] - lse : v[k][j] / s);
-            store_packet_nt<T>(yr + q * N, p);
+            for (int j = 0; j < N; ++j) o[j] = log ? v[k][j] - lse : v[k][j] * inv;
+            store_raw_nt(yr + q * N, pack<T>(o));
         }
     }
 }
 
-template <typename T, int WAVES, int VPT>
+// The backward keeps the two rows as raw packets (16-bit storage takes half
+// the registers of unpacked floats) and converts them on use.
+template <typename T, int WAVES, int EPT>
 __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_backward_rows_kernel(
     const typename Elem<T>::storage* y, const typename Elem<T>::storage* dy,
     typename Elem<T>::storage* dx, int64_t rows, int64_t D, bool log) {
     constexpr int N = Packet<T>::N;
-    constexpr int kRowsPerBlock = WAVES == 1 ? kBlock / kWave : 1;
+    constexpr int VPT = EPT / N;
+    static_assert(VPT * N == EPT, "EPT must be a whole number of packets");
     constexpr int kThreads = WAVES * kWave;
-    __shared__ float scratch[WAVES > 1 ? WAVES : 1];
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock +
-                        (WAVES == 1 ? threadIdx.x / kWave : 0);
-    const int tid = WAVES == 1 ? threadIdx.x % kWave : threadIdx.x;
+    __shared__ float scratch[block_threads<WAVES>() / kWave];
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block<WAVES>() +
+                        threadIdx.x / kThreads;
+    const int tid = threadIdx.x % kThreads;
     const bool active = row < rows;
     const int64_t npk = D / N;
     const int64_t base = (active ? row : 0) * D;
-    float a[VPT][N], g[VPT][N];
+    uint4 ry[VPT], rg[VPT];
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
         if (active && q < npk) {
-            const Packet<T> py = load_packet_nt<T>(y + base + q * N);
-            const Packet<T> pg = load_packet_nt<T>(dy + base + q * N);
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                a[k][j] = Elem<T>::load(py.v[j]);
-                g[k][j] = Elem<T>::load(pg.v[j]);
-                s += log ? g[k][j] : g[k][j] * a[k][j];
-            }
+            ry[k] = load_raw_nt(y + base + q * N);
+            rg[k] = load_raw_nt(dy + base + q * N);
         } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) a[k][j] = g[k][j] = 0.0f;
+            ry[k] = rg[k] = make_uint4(0, 0, 0, 0);  // zeros add nothing to the sum
         }
+    }
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        float a[N], g[N];
+        unpack<T>(ry[k], a);
+        unpack<T>(rg[k], g);
+#pragma unroll
+        for (int j = 0; j < N; ++j) s += log ? g[j] : g[j] * a[j];
     }
     s = row_reduce<WAVES, false>(s, scratch);
     if (!active) return;
@@ -156,44 +180,28 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_backward_rows_
     for (int k = 0; k < VPT; ++k) {
         const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
         if (q < npk) {
-            Packet<T> p;
+            float a[N], g[N], o[N];
+            unpack<T>(ry[k], a);
+            unpack<T>(rg[k], g);
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                const float r = log ? g[k][j] - expf(a[k][j]) * s : a[k][j] * (g[k][j] - s);
-                p.v[j] = Elem<T>::store(r);
+                o[j] = log ? g[j] - exp_fast(a[j]) * s : a[j] * (g[j] - s);
             }
-            store_packet_nt<T>(dx + base + q * N, p);
+            store_raw_nt(dx + base + q * N, pack<T>(o));
         }
     }
 }
 
-// Any row length: block per row, running (max, sum) in one read, results in
-// a second.  Used for rows not a multiple of the packet or beyond the
-// register-resident configs.
+// (max, sum) pairs: the sum is relative to the max.
 __device__ __forceinline__ void online_merge(float& m, float& s, float m2, float s2) {
     const float mn = fmaxf(m, m2);
     if (mn == -INFINITY) return;  // both empty
-    s = s * expf(m - mn) + s2 * expf(m2 - mn);
+    s = s * exp_fast(m - mn) + s2 * exp_fast(m2 - mn);
     m = mn;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void softmax_rows_generic_kernel(
-    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t D, bool log) {
+__device__ __forceinline__ void block_merge(float& m, float& s) {
     __shared__ float sm[kBlock / kWave], ss[kBlock / kWave];
-    const int64_t row = blockIdx.x;
-    const typename Elem<T>::storage* xr = x + row * D;
-    float m = -INFINITY, s = 0.0f;
-    for (int64_t j = threadIdx.x; j < D; j += kBlock) {
-        const float v = Elem<T>::load(xr[j]);
-        if (v == -INFINITY) continue;  // contributes exp(-inf) = 0
-        if (v > m) {
-            s = s * expf(m - v) + 1.0f;
-            m = v;
-        } else {
-            s += expf(v - m);
-        }
-    }
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
         const float m2 = wave_shfl_xor(m, o), s2 = wave_shfl_xor(s, o);
@@ -207,13 +215,128 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_generic_kernel(
     __syncthreads();
     m = sm[0];
     s = ss[0];
+#pragma unroll
     for (int w = 1; w < kBlock / kWave; ++w) online_merge(m, s, sm[w], ss[w]);
+}
+
+// Long rows (D a multiple of the packet, 16-byte aligned): a 256-thread
+// block per row.  Pass 1 keeps a running (max, sum) per thread, UNROLL
+// packets in flight; pass 2 re-reads the row (an L2 hit: the CU's current
+// row is the most recent data it touched) and writes the result.
+template <typename T, int UNROLL>
+__global__ __launch_bounds__(kBlock) void softmax_rows_long_kernel(
+    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t D, bool log) {
+    constexpr int N = Packet<T>::N;
+    const int64_t npk = D / N;
+    const typename Elem<T>::storage* xr = x + static_cast<int64_t>(blockIdx.x) * D;
+    float m = -INFINITY, s = 0.0f;
+    for (int64_t q0 = threadIdx.x; q0 < npk; q0 += static_cast<int64_t>(kBlock) * UNROLL) {
+        uint4 raw[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t q = q0 + static_cast<int64_t>(u) * kBlock;
+            raw[u] = q < npk ? *reinterpret_cast<const uint4*>(xr + q * N)
+                             : make_uint4(0xff800000u, 0xff800000u, 0xff800000u, 0xff800000u);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t q = q0 + static_cast<int64_t>(u) * kBlock;
+            if (q >= npk) continue;
+            float v[N];
+            unpack<T>(raw[u], v);
+            float pm = v[0];
+#pragma unroll
+            for (int j = 1; j < N; ++j) pm = fmaxf(pm, v[j]);
+            const float mn = fmaxf(m, pm);
+            if (mn == -INFINITY) continue;
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) t += exp_fast(v[j] - mn);
+            s = s * exp_fast(m - mn) + t;
+            m = mn;
+        }
+    }
+    block_merge(m, s);
     const float shift = m == -INFINITY ? 0.0f : m;
     const float lse = logf(s);
+    const float inv = 1.0f / s;
+    typename Elem<T>::storage* yr = y + static_cast<int64_t>(blockIdx.x) * D;
+    for (int64_t q = threadIdx.x; q < npk; q += kBlock) {
+        float v[N], o[N];
+        unpack<T>(*reinterpret_cast<const uint4*>(xr + q * N), v);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const float d = v[j] - shift;
+            o[j] = log ? d - lse : exp_fast(d) * inv;
+        }
+        store_raw_nt(yr + q * N, pack<T>(o));
+    }
+}
+
+template <typename T, int UNROLL>
+__global__ __launch_bounds__(kBlock) void softmax_backward_rows_long_kernel(
+    const typename Elem<T>::storage* y, const typename Elem<T>::storage* dy,
+    typename Elem<T>::storage* dx, int64_t D, bool log) {
+    constexpr int N = Packet<T>::N;
+    __shared__ float scratch[kBlock / kWave];
+    const int64_t npk = D / N;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * D;
+    float s = 0.0f;
+    for (int64_t q0 = threadIdx.x; q0 < npk; q0 += static_cast<int64_t>(kBlock) * UNROLL) {
+        uint4 ra[UNROLL], rg[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int64_t q = q0 + static_cast<int64_t>(u) * kBlock;
+            const bool in = q < npk;
+            ra[u] = in ? *reinterpret_cast<const uint4*>(y + base + q * N) : make_uint4(0, 0, 0, 0);
+            rg[u] = in ? *reinterpret_cast<const uint4*>(dy + base + q * N) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            float a[N], g[N];
+            unpack<T>(ra[u], a);
+            unpack<T>(rg[u], g);
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += log ? g[j] : g[j] * a[j];
+        }
+    }
+    s = row_reduce<kBlock / kWave, false>(s, scratch);
+    for (int64_t q = threadIdx.x; q < npk; q += kBlock) {
+        float a[N], g[N], o[N];
+        unpack<T>(*reinterpret_cast<const uint4*>(y + base + q * N), a);
+        unpack<T>(*reinterpret_cast<const uint4*>(dy + base + q * N), g);
+#pragma unroll
+        for (int j = 0; j < N; ++j) o[j] = log ? g[j] - exp_fast(a[j]) * s : a[j] * (g[j] - s);
+        store_raw_nt(dx + base + q * N, pack<T>(o));
+    }
+}
+
+// Any row length or alignment: block per row, running (max, sum) in one
+// read, results in a second.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void softmax_rows_generic_kernel(
+    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t D, bool log) {
+    const int64_t row = blockIdx.x;
+    const typename Elem<T>::storage* xr = x + row * D;
+    float m = -INFINITY, s = 0.0f;
+    for (int64_t j = threadIdx.x; j < D; j += kBlock) {
+        const float v = Elem<T>::load(xr[j]);
+        if (v == -INFINITY) continue;  // contributes exp(-inf) = 0
+        if (v > m) {
+            s = s * exp_fast(m - v) + 1.0f;
+            m = v;
+        } else {
+            s += exp_fast(v - m);
+        }
+    }
+    block_merge(m, s);
+    const float shift = m == -INFINITY ? 0.0f : m;
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
     typename Elem<T>::storage* yr = y + row * D;
     for (int64_t j = threadIdx.x; j < D; j += kBlock) {
-        const float v = Elem<T>::load(xr[j]) - shift;
-        yr[j] = Elem<T>::store(log ? v - lse : expf(v) / s);
+        const float d = Elem<T>::load(xr[j]) - shift;
+        yr[j] = Elem<T>::store(log ? d - lse : exp_fast(d) * inv);
     }
 }
 
@@ -231,7 +354,7 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_rows_generic_kernel(
     s = row_reduce<kBlock / kWave, false>(s, scratch);
     for (int64_t j = threadIdx.x; j < D; j += kBlock) {
         const float a = Elem<T>::load(y[base + j]), g = Elem<T>::load(dy[base + j]);
-        dx[base + j] = Elem<T>::store(log ? g - expf(a) * s : a * (g - s));
+        dx[base + j] = Elem<T>::store(log ? g - exp_fast(a) * s : a * (g - s));
     }
 }
 
@@ -251,17 +374,18 @@ __global__ __launch_bounds__(kBlock) void softmax_strided_kernel(
             const float v = Elem<T>::load(x[base + d * inner]);
             if (v == -INFINITY) continue;  // contributes exp(-inf) = 0
             if (v > m) {
-                s = s * expf(m - v) + 1.0f;
+                s = s * exp_fast(m - v) + 1.0f;
                 m = v;
             } else {
-                s += expf(v - m);
+                s += exp_fast(v - m);
             }
         }
         const float shift = m == -INFINITY ? 0.0f : m;
         const float lse = logf(s);
+        const float inv = 1.0f / s;
         for (int64_t d = 0; d < D; ++d) {
             const float v = Elem<T>::load(x[base + d * inner]) - shift;
-            y[base + d * inner] = Elem<T>::store(log ? v - lse : expf(v) / s);
+            y[base + d * inner] = Elem<T>::store(log ? v - lse : exp_fast(v) * inv);
         }
     }
 }
@@ -284,73 +408,85 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_strided_kernel(
         for (int64_t d = 0; d < D; ++d) {
             const float a = Elem<T>::load(y[base + d * inner]);
             const float g = Elem<T>::load(dy[base + d * inner]);
-            dx[base + d * inner] = Elem<T>::store(log ? g - expf(a) * s : a * (g - s));
+            dx[base + d * inner] = Elem<T>::store(log ? g - exp_fast(a) * s : a * (g - s));
         }
     }
 }
 
-// Register-resident configurations (WAVES, VPT), smallest capacity first.
-struct RowConfig {
-    int waves, vpt;
-};
-constexpr RowConfig kForwardConfigs[] = {{1, 1}, {1, 2}, {1, 4},  {1, 8},  {1, 16},
-                                         {4, 8}, {4, 16}, {16, 8}, {16, 16}};
-constexpr RowConfig kBackwardConfigs[] = {{1, 1}, {1, 2}, {1, 4}, {1, 8},
-                                          {4, 4}, {4, 8}, {16, 4}, {16, 8}};
+// ---- configuration choice ---------------------------------------------------
 
-template <typename T, int W, int V>
+// A register-resident layout; waves == 0 means the long-row kernel.
+struct RowConfig {
+    int waves, ept;
+};
+
+template <typename T, int W, int E>
 void launch_forward_rows(int device, const void* x, void* y, int64_t rows, int64_t D, bool log) {
     using S = typename Elem<T>::storage;
-    constexpr int rows_per_block = W == 1 ? kBlock / kWave : 1;
-    const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-    softmax_rows_kernel<T, W, V><<<blocks, block_threads<W>(), 0, stream(device)>>>(
+    const int64_t blocks = (rows + rows_per_block<W>() - 1) / rows_per_block<W>();
+    softmax_rows_kernel<T, W, E><<<blocks, block_threads<W>(), 0, stream(device)>>>(
         static_cast<const S*>(x), static_cast<S*>(y), rows, D, log);
 }
 
-template <typename T, int W, int V>
+template <typename T, int W, int E>
 void launch_backward_rows(int device, const void* y, const void* dy, void* dx, int64_t rows,
                           int64_t D, bool log) {
     using S = typename Elem<T>::storage;
-    constexpr int rows_per_block = W == 1 ? kBlock / kWave : 1;
-    const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-    softmax_backward_rows_kernel<T, W, V><<<blocks, block_threads<W>(), 0, stream(device)>>>(
+    const int64_t blocks = (rows + rows_per_block<W>() - 1) / rows_per_block<W>();
+    softmax_backward_rows_kernel<T, W, E><<<blocks, block_threads<W>(), 0, stream(device)>>>(
         static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), rows, D, log);
 }
 
+// The layouts compiled, as (waves per row, packets per thread): the
+// measured best on MI355X puts about two 16-byte packets in each thread and
+// grows the number of waves with the row, up to 16 (a 1024-thread block);
+// longer rows then take more packets per thread, up to 32 float32 values.
+#define TP_AMD_SOFTMAX_CONFIGS(X) \
+    X(1, 1) X(1, 2) X(2, 2) X(4, 2) X(8, 2) X(16, 2) X(16, 4) X(16, 8)
+
 template <typename T>
-bool forward_rows_resident(int device, const void* x, void* y, int64_t rows, int64_t D,
-                           bool log) {
+bool launch_forward_config(RowConfig c, int device, const void* x, void* y, int64_t rows,
+                           int64_t D, bool log) {
     constexpr int N = Packet<T>::N;
-    for (const RowConfig& c : kForwardConfigs) {
-        if (static_cast<int64_t>(c.waves) * kWave * c.vpt * N < D) continue;
-#define TP_AMD_FWD(W, V)                                                            \
-    if (c.waves == W && c.vpt == V) {                                               \
-        launch_forward_rows<T, W, V>(device, x, y, rows, D, log);                   \
-        return true;                                                                \
+#define TP_AMD_FWD(W, V)                                                             \
+    if constexpr (V * N <= 32) {                                                     \
+        if (c.waves == W && c.ept == V * N) {                                        \
+            launch_forward_rows<T, W, V * N>(device, x, y, rows, D, log);            \
+            return true;                                                             \
+        }                                                                            \
     }
-        TP_AMD_FWD(1, 1) TP_AMD_FWD(1, 2) TP_AMD_FWD(1, 4) TP_AMD_FWD(1, 8) TP_AMD_FWD(1, 16)
-        TP_AMD_FWD(4, 8) TP_AMD_FWD(4, 16) TP_AMD_FWD(16, 8) TP_AMD_FWD(16, 16)
+    TP_AMD_SOFTMAX_CONFIGS(TP_AMD_FWD)
 #undef TP_AMD_FWD
-    }
     return false;
 }
 
 template <typename T>
-bool backward_rows_resident(int device, const void* y, const void* dy, void* dx, int64_t rows,
-                            int64_t D, bool log) {
+bool launch_backward_config(RowConfig c, int device, const void* y, const void* dy, void* dx,
+                            int64_t rows, int64_t D, bool log) {
     constexpr int N = Packet<T>::N;
-    for (const RowConfig& c : kBackwardConfigs) {
-        if (static_cast<int64_t>(c.waves) * kWave * c.vpt * N < D) continue;
-#define TP_AMD_BWD(W, V)                                                            \
-    if (c.waves == W && c.vpt == V) {                                               \
-        launch_backward_rows<T, W, V>(device, y, dy, dx, rows, D, log);             \
-        return true;                                                                \
+#define TP_AMD_BWD(W, V)                                                             \
+    if constexpr (V * N <= 32) {                                                     \
+        if (c.waves == W && c.ept == V * N) {                                        \
+            launch_backward_rows<T, W, V * N>(device, y, dy, dx, rows, D, log);      \
+            return true;                                                             \
+        }                                                                            \
     }
-        TP_AMD_BWD(1, 1) TP_AMD_BWD(1, 2) TP_AMD_BWD(1, 4) TP_AMD_BWD(1, 8)
-        TP_AMD_BWD(4, 4) TP_AMD_BWD(4, 8) TP_AMD_BWD(16, 4) TP_AMD_BWD(16, 8)
+    TP_AMD_SOFTMAX_CONFIGS(TP_AMD_BWD)
 #undef TP_AMD_BWD
-    }
     return false;
+}
+
+// The compiled layout for a row of D elements (waves == 0: none holds it).
+template <typename T>
+RowConfig choose_config(int64_t D) {
+    constexpr int N = Packet<T>::N;
+    constexpr int kPairs[][2] = {{1, 1}, {1, 2}, {2, 2}, {4, 2}, {8, 2}, {16, 2}, {16, 4}, {16, 8}};
+    const int64_t npk = (D + N - 1) / N;
+    for (const auto& c : kPairs) {
+        if (c[1] * N > 32) break;
+        if (static_cast<int64_t>(c[0]) * kWave * c[1] >= npk) return RowConfig{c[0], c[1] * N};
+    }
+    return RowConfig{0, 0};
 }
 
 int64_t strided_grid(int64_t total, int device) {
@@ -367,7 +503,16 @@ void softmax_typed(int device, bool log, int64_t outer, int64_t D, int64_t inner
     hipStream_t st = stream(device);
     if (inner == 1) {
         const bool vec = D % N == 0 && aligned16(x) && aligned16(y);
-        if (!(vec && forward_rows_resident<T>(device, x, y, outer, D, log))) {
+        const RowConfig c = choose_config<T>(D);
+        // 16-bit rows that need 16 waves run faster through the long-row
+        // kernel (their 1024-thread blocks leave a CU one row at a time).
+        const bool long_row = sizeof(S) == 2 && D / N > 16 * kWave * 2;
+        if (vec && c.waves > 0 && !long_row) {
+            launch_forward_config<T>(c, device, x, y, outer, D, log);
+        } else if (vec) {
+            softmax_rows_long_kernel<T, 4><<<outer, kBlock, 0, st>>>(
+                static_cast<const S*>(x), static_cast<S*>(y), D, log);
+        } else {
             softmax_rows_generic_kernel<T><<<outer, kBlock, 0, st>>>(
                 static_cast<const S*>(x), static_cast<S*>(y), D, log);
         }
@@ -386,7 +531,13 @@ void softmax_backward_typed(int device, bool log, int64_t outer, int64_t D, int6
     hipStream_t st = stream(device);
     if (inner == 1) {
         const bool vec = D % N == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
-        if (!(vec && backward_rows_resident<T>(device, y, dy, dx, outer, D, log))) {
+        const RowConfig c = choose_config<T>(D);
+        if (vec && c.waves > 0) {
+            launch_backward_config<T>(c, device, y, dy, dx, outer, D, log);
+        } else if (vec) {
+            softmax_backward_rows_long_kernel<T, 2><<<outer, kBlock, 0, st>>>(
+                static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), D, log);
+        } else {
             softmax_backward_rows_generic_kernel<T><<<outer, kBlock, 0, st>>>(
                 static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), D, log);
         }

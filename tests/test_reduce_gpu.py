@@ -112,6 +112,37 @@ def test_reduction_edge_cases(dev, ops, orc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim", [0, 1])
+def test_amax_amin_nan_and_signed_zero_vectorised(dev, ops, orc, dtype, dim):
+    """The packet paths of both reduction kernels (rows and columns) with NaN,
+    all-NaN, signed-zero and all-negative lines mixed into random data."""
+    g = np.random.default_rng(11)
+    x = g.standard_normal((96, 4096)).astype(np.float32)
+    x[3, 17] = np.nan                       # one NaN among numbers
+    x[5, :] = np.nan                        # all NaN
+    x[7, :] = -0.0                          # only -0
+    x[9, :] = 0.0
+    x[9, ::2] = -0.0                        # -0 and +0 mixed
+    x[11, :] = -np.abs(x[11, :]) - 1.0      # all negative
+    x[13, g.integers(0, 4096, 64)] = np.nan
+    x[:, 21] = np.nan                       # a NaN column
+    x[:, 23] = -0.0
+    x[:, 25] = 0.0
+    x[::3, 25] = -0.0
+    x[:, 27] = np.nan
+    x[40, 27] = -5.0                        # a single number in a NaN column
+    a = orc.from_float(x, dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
+        got = fn(d, [dim]).numpy()
+        want = oracle_reduce(orc, op, dtype, a, [dim])
+        gf, wf = orc.to_float(got, dtype), orc.to_float(want, dtype)
+        assert np.array_equal(np.isnan(gf), np.isnan(wf)), (op, dim)
+        ok = ~np.isnan(wf)
+        assert_bitexact(got[ok], want[ok], f"op {op} dim {dim}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("dim", [0, 1, -1])
 def test_softmax_and_log_softmax(dev, ops, orc, dtype, dim):
     a = sample(orc, (5, 6, 7), dtype)
