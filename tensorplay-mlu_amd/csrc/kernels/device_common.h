@@ -219,4 +219,28 @@ __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, kWave);
 }
 
+// Lane value rotated right by N within each row of 16 lanes (DPP row_ror).
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf,
+                                                      false));
+}
+
+// Reduction of v over the 64 lanes of the wave with an associative and
+// commutative op, returned to every lane: four DPP rotations combine each
+// row of 16 lanes, then the four row results are read as scalars.  A
+// handful of cycles, where a shuffle ladder pays LDS latency six times.
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce(float v, Op op) {
+    v = op(v, row_ror<8>(v));
+    v = op(v, row_ror<4>(v));
+    v = op(v, row_ror<2>(v));
+    v = op(v, row_ror<1>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return op(op(a, b), op(c, d));
+}
+
 }  // namespace tp_amd

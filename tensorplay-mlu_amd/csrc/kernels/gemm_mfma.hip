@@ -223,7 +223,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
     const int half = lane / 32, l32 = lane % 32;
     const int64_t nk = (p.k + BK - 1) / BK;
 
-    for (int64_t bi = blockIdx.z; bi < p.batch; bi += gridDim.z) {
+    // One batch entry per blockIdx.z (the host launches batches of at most
+    // 65535); a loop over the batch here would keep every address live
+    // across it and spill.
+    {
+        const int64_t bi = blockIdx.z;
         const S* A = static_cast<const S*>(p.a) + bi * p.stride_a;
         const S* B = static_cast<const S*>(p.b) + bi * p.stride_b;
         f32x16 acc[TM][TN];
@@ -249,25 +253,34 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
         for (int64_t kt = 0; kt < nk; ++kt) {
             const S* As = lds + (kt & 1) * STAGE;
             const S* Bs = As + BM * LDS_STRIDE;
-#pragma unroll 2
-            for (int s = 0; s < BK / KSUB; ++s) {
-                uint4 af[TM], bf[TN];
+            // Fragments are double-buffered across the K substeps: the LDS
+            // reads for substep s + 1 are issued before the MFMAs of s, so
+            // their latency hides behind the matrix work.
+            constexpr int NSUB = BK / KSUB;
+            uint4 af[2][TM], bf[2][TN];
+            auto fetch = [&](int s, int buf) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
                     const int row = wm * kWaveM + i * 32 + l32;
-                    af[i] = *reinterpret_cast<const uint4*>(As + row * LDS_STRIDE + s * KSUB +
-                                                            half * (KSUB / 2));
+                    af[buf][i] = *reinterpret_cast<const uint4*>(As + row * LDS_STRIDE + s * KSUB +
+                                                                 half * (KSUB / 2));
                 }
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const int col = wn * kWaveN + j * 32 + l32;
-                    bf[j] = *reinterpret_cast<const uint4*>(Bs + col * LDS_STRIDE + s * KSUB +
-                                                            half * (KSUB / 2));
+                    bf[buf][j] = *reinterpret_cast<const uint4*>(Bs + col * LDS_STRIDE + s * KSUB +
+                                                                 half * (KSUB / 2));
                 }
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s) {
+                if (s + 1 < NSUB) fetch(s + 1, (s + 1) & 1);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[i], bf[j], acc[i][j]);
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = Mfma<T>::mma(af[s & 1][i], bf[s & 1][j], acc[i][j]);
             }
             // The other stage was last read in step kt - 1, before the
             // barrier that ended it: fill it with K tile kt + 1 and start
@@ -307,6 +320,19 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
                         }
                         cp += 8 * p.ldc;
                     }
+                } else if (p.cin_rs == 0) {
+                    // A bias along N (addmm / linear): one value per column.
+                    const float c = p.beta * Elem<T>::load(Cin[bi * p.cin_stride_b + col * p.cin_cs]);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (rbase + 8 * g + r < p.m) {
+                                cp[r * p.ldc] = Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c));
+                            }
+                        }
+                        cp += 8 * p.ldc;
+                    }
                 } else {
                     const S* ci = Cin + bi * p.cin_stride_b + rbase * p.cin_rs + col * p.cin_cs;
 #pragma unroll
@@ -340,11 +366,10 @@ bool mfma_eligible(const GemmArgs& p) {
 }
 
 template <typename T, int BM, int BN, int WM, int WN>
-void launch_config(const GemmArgs& p, hipStream_t stream) {
+void launch_chunk(const GemmArgs& p, hipStream_t stream) {
     constexpr int THREADS = WM * WN * kWave;
     const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
-    const dim3 grid(static_cast<unsigned>(tiles), 1u,
-                    static_cast<unsigned>(p.batch < 65535 ? p.batch : 65535));
+    const dim3 grid(static_cast<unsigned>(tiles), 1u, static_cast<unsigned>(p.batch));
     const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
     if (a_kmajor && b_kmajor) {
         gemm_mfma_kernel<T, true, true, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
@@ -358,6 +383,20 @@ void launch_config(const GemmArgs& p, hipStream_t stream) {
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
+template <typename T, int BM, int BN, int WM, int WN>
+void launch_config(const GemmArgs& whole, hipStream_t stream) {
+    constexpr int64_t kMaxZ = 65535;
+    using S = typename Elem<T>::storage;
+    for (int64_t b0 = 0; b0 < whole.batch; b0 += kMaxZ) {
+        GemmArgs p = whole;
+        p.batch = whole.batch - b0 < kMaxZ ? whole.batch - b0 : kMaxZ;
+        p.a = static_cast<const S*>(whole.a) + b0 * whole.stride_a;
+        p.b = static_cast<const S*>(whole.b) + b0 * whole.stride_b;
+        p.c = static_cast<S*>(whole.c) + b0 * whole.stride_c;
+        if (whole.cin != nullptr) p.cin = static_cast<const S*>(whole.cin) + b0 * whole.cin_stride_b;
+        launch_chunk<T, BM, BN, WM, WN>(p, stream);
+    }
+}
 // 16-bit types take the big tile when it still gives every CU a block;
 // float32 (bound by its much slower MFMA rate) keeps the small one, whose
 // registers fit without spilling.

@@ -63,11 +63,7 @@ struct Combine<TP_AMD_REDUCE_AMIN> {
 
 template <int OP>
 __device__ __forceinline__ float wave_reduce(float v) {
-#pragma unroll
-    for (int mask = kWave / 2; mask > 0; mask >>= 1) {
-        v = Combine<OP>::apply(v, wave_shfl_xor(v, mask));
-    }
-    return v;
+    return wave_allreduce(v, [](float a, float b) { return Combine<OP>::apply(a, b); });
 }
 
 // ---- amax / amin on order-preserving integer keys -------------------------------
@@ -250,7 +246,7 @@ __device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
                                           const typename Elem<Tin>::storage* p, int64_t row0,
                                           int64_t end, int64_t inner) {
     constexpr int G = kBlock / 64;  // row groups
-    constexpr int U = 4;
+    constexpr int U = 8;
     using K = KeyOps<OP>;
     constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
     int32_t k32[4];
@@ -324,7 +320,7 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
         if (exact && col < inner) {
             const typename Elem<Tin>::storage* p = x + o * r * inner + col;
             int64_t row = begin + rg;
-            constexpr int U = 4;
+            constexpr int U = 8;
             for (; row + (U - 1) * kRowGroups < end; row += U * kRowGroups) {
                 if constexpr (VEC) {
                     Packet<Tin> v[U];
@@ -445,7 +441,9 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     const int64_t bx = (inner + cols_per_block - 1) / cols_per_block;
     const int64_t z = outer < 65535 ? outer : 65535;
     const int64_t base_blocks = bx * z;
-    const int64_t target_blocks = cus * 8;
+    // Two blocks per CU, each with eight 16-byte loads per thread in flight,
+    // keep HBM busy; more chunks would only grow the second pass.
+    const int64_t target_blocks = cus * 2;
     int64_t nchunk = 1;
     if (base_blocks < target_blocks && r >= 64) {
         nchunk = (target_blocks + base_blocks - 1) / base_blocks;

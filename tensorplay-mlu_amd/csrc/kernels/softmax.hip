@@ -22,6 +22,7 @@
 // conversions.
 
 #include <cmath>
+#include <type_traits>
 
 #include "device_common.h"
 #include "../runtime.h"
@@ -39,14 +40,10 @@ constexpr float kLog2e = 1.44269504088896340736f;
 __device__ __forceinline__ float exp_fast(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = kWave / 2; m > 0; m >>= 1) v = fmaxf(v, wave_shfl_xor(v, m));
-    return v;
+    return wave_allreduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = kWave / 2; m > 0; m >>= 1) v += wave_shfl_xor(v, m);
-    return v;
+    return wave_allreduce(v, [](float a, float b) { return a + b; });
 }
 
 // Layout of a (WAVES, EPT) configuration: WAVES <= 4 packs 4 / WAVES rows
@@ -134,6 +131,144 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_rows_kernel(
             for (int j = 0; j < N; ++j) o[j] = log ? v[k][j] - lse : v[k][j] * inv;
             store_raw_nt(yr + q * N, pack<T>(o));
         }
+    }
+}
+
+// Rows that need a whole 16-wave block: one such block fills a CU, so a
+// block per row would leave the CU idle while each row's loads are in
+// flight.  Instead a grid of one block per CU walks the rows, and the loads
+// of its next row are issued before the current row is reduced and written
+// (two register sets, alternating).
+template <typename T, int VPT>
+struct RowBuffer {
+    uint4 raw[VPT];
+};
+
+template <typename T, int VPT>
+__device__ __forceinline__ void fetch_row(RowBuffer<T, VPT>& b,
+                                          const typename Elem<T>::storage* xr, int64_t npk,
+                                          int tid) {
+    constexpr int N = Packet<T>::N;
+    // -inf in the storage format pads the packets past the row's end.
+    constexpr uint32_t kNegInf = sizeof(typename Elem<T>::storage) == 4 ? 0xff800000u
+                                 : std::is_same_v<T, bf16_t>           ? 0xff80ff80u
+                                                                       : 0xfc00fc00u;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
+        b.raw[k] = q < npk ? load_raw_nt(xr + q * N) : make_uint4(kNegInf, kNegInf, kNegInf, kNegInf);
+    }
+}
+
+__device__ __forceinline__ uint32_t& word(uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// float32 rows work in place in the packet registers (a second float copy
+// of the row would not fit beside the prefetched next row).
+template <int VPT>
+__device__ __forceinline__ void finish_row_f32(RowBuffer<float, VPT>& b, float* yr, int64_t npk,
+                                               int tid, bool log, float* scratch) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, __uint_as_float(word(b.raw[k], j)));
+    m = row_reduce<16, true>(m, scratch);
+    const float shift = m == -INFINITY ? 0.0f : m;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float d = __uint_as_float(word(b.raw[k], j)) - shift;
+            const float e = exp_fast(d);
+            s += e;
+            word(b.raw[k], j) = __float_as_uint(log ? d : e);
+        }
+    s = row_reduce<16, false>(s, scratch);
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
+        if (q < npk) {
+            uint4 o = b.raw[k];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = __uint_as_float(word(o, j));
+                word(o, j) = __float_as_uint(log ? v - lse : v * inv);
+            }
+            store_raw_nt(yr + q * 4, o);
+        }
+    }
+}
+
+template <typename T, int VPT>
+__device__ __forceinline__ void finish_row(RowBuffer<T, VPT>& b,
+                                           typename Elem<T>::storage* yr, int64_t npk, int tid,
+                                           bool log, float* scratch) {
+    if constexpr (sizeof(typename Elem<T>::storage) == 4) {
+        finish_row_f32<VPT>(b, yr, npk, tid, log, scratch);
+        return;
+    }
+    constexpr int N = Packet<T>::N;
+    float v[VPT][N];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        unpack<T>(b.raw[k], v[k]);
+#pragma unroll
+        for (int j = 0; j < N; ++j) m = fmaxf(m, v[k][j]);
+    }
+    m = row_reduce<16, true>(m, scratch);
+    const float shift = m == -INFINITY ? 0.0f : m;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            v[k][j] -= shift;
+            const float e = exp_fast(v[k][j]);
+            s += e;
+            if (!log) v[k][j] = e;
+        }
+    s = row_reduce<16, false>(s, scratch);
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
+        if (q < npk) {
+            float o[N];
+#pragma unroll
+            for (int j = 0; j < N; ++j) o[j] = log ? v[k][j] - lse : v[k][j] * inv;
+            store_raw_nt(yr + q * N, pack<T>(o));
+        }
+    }
+}
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(16 * kWave) void softmax_rows_stream_kernel(
+    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t rows, int64_t D,
+    bool log) {
+    constexpr int N = Packet<T>::N;
+    __shared__ float scratch[16];
+    const int tid = threadIdx.x;
+    const int64_t npk = D / N;
+    const int64_t step = gridDim.x;
+    RowBuffer<T, VPT> a, b;
+    int64_t row = blockIdx.x;
+    if (row < rows) fetch_row<T, VPT>(a, x + row * D, npk, tid);
+    // Uniform per block: every thread walks the same rows.
+    while (row < rows) {
+        if (row + step < rows) fetch_row<T, VPT>(b, x + (row + step) * D, npk, tid);
+        finish_row<T, VPT>(a, y + row * D, npk, tid, log, scratch);
+        row += step;
+        if (row >= rows) break;
+        if (row + step < rows) fetch_row<T, VPT>(a, x + (row + step) * D, npk, tid);
+        finish_row<T, VPT>(b, y + row * D, npk, tid, log, scratch);
+        row += step;
     }
 }
 
@@ -504,10 +639,21 @@ void softmax_typed(int device, bool log, int64_t outer, int64_t D, int64_t inner
     if (inner == 1) {
         const bool vec = D % N == 0 && aligned16(x) && aligned16(y);
         const RowConfig c = choose_config<T>(D);
-        // 16-bit rows that need 16 waves run faster through the long-row
-        // kernel (their 1024-thread blocks leave a CU one row at a time).
-        const bool long_row = sizeof(S) == 2 && D / N > 16 * kWave * 2;
-        if (vec && c.waves > 0 && !long_row) {
+        if (vec && c.waves == 16) {
+            // Rows that need a whole block: one block per CU walks them.
+            const int64_t grid = outer < cu_count(device) ? outer : cu_count(device);
+            const int vpt = c.ept / N;
+            if (vpt <= 2) {
+                softmax_rows_stream_kernel<T, 2><<<grid, 16 * kWave, 0, st>>>(
+                    static_cast<const S*>(x), static_cast<S*>(y), outer, D, log);
+            } else if (vpt <= 4) {
+                softmax_rows_stream_kernel<T, 4><<<grid, 16 * kWave, 0, st>>>(
+                    static_cast<const S*>(x), static_cast<S*>(y), outer, D, log);
+            } else if constexpr (N == 4) {
+                softmax_rows_stream_kernel<T, 8><<<grid, 16 * kWave, 0, st>>>(
+                    static_cast<const S*>(x), static_cast<S*>(y), outer, D, log);
+            }
+        } else if (vec && c.waves > 0) {
             launch_forward_config<T>(c, device, x, y, outer, D, log);
         } else if (vec) {
             softmax_rows_long_kernel<T, 4><<<outer, kBlock, 0, st>>>(

@@ -178,6 +178,19 @@ def test_softmax_row_lengths(dev, ops, orc, D):
                             dtype, 1, f"backward D={D} log={log}")
 
 
+@pytest.mark.parametrize("rows,D,dtype", [(600, 8200, F32), (1000, 20000, F32), (257, 32000, F32),
+                                          (600, 16400, BF16), (513, 30000, BF16)])
+def test_softmax_rows_walked_by_one_block_per_cu(dev, ops, orc, rows, D, dtype):
+    """Rows needing a 16-wave block are walked by a grid of one block per CU
+    with the next row prefetched: more rows than CUs, odd row counts."""
+    a = sample(orc, (rows, D), dtype, 5, 3.0)
+    d = dev.from_numpy(a, dtype=dtype)
+    for log in (False, True):
+        y = (ops.log_softmax if log else ops.softmax)(d, -1)
+        assert_normwise(y.numpy(), orc.softmax(log, dtype, a, rows, D, 1), dtype, 1,
+                        f"rows={rows} D={D} log={log}")
+
+
 def test_softmax_declines(dev, ops, orc):
     tensor = __import__("importlib").import_module("tensorplay-mlu_amd.tensor")
     a = dev.from_numpy(sample(orc, (4, 5), F32))
