@@ -23,6 +23,7 @@ Also reported on the same line:
   sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
+  python bench.py --profile {traffic,gemm,reduce}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -40,6 +41,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3's
+# FETCH_SIZE and WRITE_SIZE counters (one pass each over
+# ``bench.py --profile traffic``), each scaled by what the same counter reads
+# for a copy kernel of known size; recorded in
+# profiles/config2_binary2d_hbm_traffic.md.
+DOMINANT_TRAFFIC_BYTES = 536960288
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
 METRIC = "GEMM TFLOP/s + %MFMA peak; reduce/softmax/eltwise GB/s + %HBM peak"
 N = 8192
@@ -143,7 +150,8 @@ def dominant_kernel(lib, ev, t, reps=50):
     achieved = algo / (ms * 1e-3) / 1e9
     return {"kernel": "binary2d_kernel<float, full, row-broadcast> (add)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": DOMINANT_TRAFFIC_BYTES,
             "avg_us": round(ms * 1e3, 2), "algorithmic_bytes_per_launch": algo}
 
 
@@ -323,6 +331,52 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 8):
                       "OpenMP; TensorPlay's CPU path is not installed)"}
 
 
+def profile_launches(what: str, lib, ops, dev) -> None:
+    """Fixed launch sequences for counter and trace collection under
+    rocprofv3 (``--profile``); no timing, no JSON line.
+
+    traffic: ten launches of a copy-like kernel (affine y = 1 x + 0 on
+             [8192, 8192] float32, 2 x 268,435,456 B) to calibrate the
+             FETCH_SIZE / WRITE_SIZE counters, then ten of the dominant kernel;
+    gemm:    ten bf16 4096^3 products (A, B row-major);
+    reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
+             and bf16, five each."""
+    import ctypes as C
+    if what == "traffic":
+        a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
+        row = dev.from_numpy(np.full((N,), 0.5, np.float32))
+        out = ops.empty((N, N), F32)
+        sizes = (C.c_int64 * 2)(N, N)
+        sa, sb = (C.c_int64 * 2)(N, 1), (C.c_int64 * 2)(0, 1)
+        for _ in range(10):
+            assert lib.tp_amd_launch_affine(0, F32, N * N, a.data_ptr, 1.0, 0.0, out.data_ptr) == 0
+        for _ in range(10):
+            assert lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, a.data_ptr, sa, row.data_ptr, sb,
+                                            out.data_ptr, sa, 1.0) == 0
+    elif what == "gemm":
+        K = 4096
+        g = np.random.default_rng(0)
+        a = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
+        b = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
+        c = ops.empty((K, K), BF16)
+        for _ in range(10):
+            assert lib.tp_amd_launch_gemm(0, BF16, 1, K, K, K, 1.0, a.data_ptr, K, 0, 0,
+                                          b.data_ptr, K, 0, 0, 0.0, None, 0, 0, 0,
+                                          c.data_ptr, K, 0) == 0
+    elif what == "reduce":
+        g = np.random.default_rng(0)
+        x32 = dev.from_numpy(g.standard_normal((32768, 4096), dtype=np.float32))
+        for x in (x32, ops.to(x32, BF16)):
+            for fn in (ops.sum_dim, ops.amax):
+                for dim in (-1, 0):
+                    for _ in range(5):
+                        fn(x, [dim])
+    else:
+        raise SystemExit(f"unknown --profile {what}")
+    assert lib.tp_amd_synchronize(0) == 0
+    log(f"bench: profile launches '{what}' done")
+
+
 def main() -> int:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -330,6 +384,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--profile", choices=["traffic", "gemm", "reduce"],
+                   help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -343,6 +399,9 @@ def main() -> int:
     if not runtime.is_available():
         print("no GPU visible", file=sys.stderr)
         return 1
+    if args.profile:
+        profile_launches(args.profile, lib, ops, dev)
+        return 0
 
     log("bench: building config-2 inputs")
     tensors = {F32: build_config2(ops, dev, F32), BF16: build_config2(ops, dev, BF16)}

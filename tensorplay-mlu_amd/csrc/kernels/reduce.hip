@@ -18,6 +18,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <type_traits>
 
 #include "device_common.h"
 #include "../allocator.h"
@@ -120,6 +121,24 @@ struct KeyOps {
     }
 };
 
+// Reduction across the wave.  amax / amin reduce the order-preserving keys
+// with integer max / min -- a lane holding NaN (no elements, or only NaNs)
+// takes the key that loses -- and decode the winner; sums add floats.
+template <int OP>
+__device__ __forceinline__ float lane_reduce(float v) {
+    if constexpr (kMinMax<OP>) {
+        using K = KeyOps<OP>;
+        const int32_t k = v != v ? K::id32() : key32(__float_as_uint(v));
+        const float r = wave_allreduce(__int_as_float(k), [](float a, float b) {
+            return __int_as_float(K::pick(__float_as_int(a), __float_as_int(b)));
+        });
+        const int32_t kr = __float_as_int(r);
+        return kr == K::id32() ? Combine<OP>::identity() : K::value32(kr);
+    } else {
+        return wave_reduce<OP>(v);
+    }
+}
+
 // Final value of a reduction: the mean divides the float32 sum by the
 // number of reduced elements.
 template <int OP>
@@ -130,34 +149,46 @@ __device__ __forceinline__ float finish(float v, int64_t count, bool final_pass)
     return v;
 }
 
+// A packet of one repeated 32-bit word (the padding of partial batches).
+__device__ __forceinline__ uint4 splat(uint32_t w) { return make_uint4(w, w, w, w); }
+
 // One thread's share of packets [pb, pe) of a row segment: packets
-// pb + tid, pb + tid + THREADS, ...  Float combine in element order.
+// pb + tid, pb + tid + THREADS, ...  Loads go out in batches of U, the
+// batch's out-of-range slots padded with a value that leaves the result
+// unchanged, so every batch's loads are in flight together.  Float combine
+// in element order.
 template <typename Tin, int OP, int THREADS>
 __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p, int64_t pb,
                                            int64_t pe, int tid) {
     constexpr int N = Packet<Tin>::N;
     constexpr int U = 4;
+    // Zeros add nothing; NaN is skipped by amax / amin.
+    constexpr uint32_t kPad = kMinMax<OP> ? (N == 4 ? 0x7fc00000u : (std::is_same_v<Tin, bf16_t>
+                                                                          ? 0x7fc07fc0u
+                                                                          : 0x7e007e00u))
+                                          : 0u;
     float acc = Combine<OP>::identity();
-    int64_t q = pb + tid;
-    for (; q + (U - 1) * THREADS < pe; q += U * THREADS) {
-        Packet<Tin> v[U];
+    for (int64_t q0 = pb + tid; q0 < pe; q0 += static_cast<int64_t>(U) * THREADS) {
+        uint4 raw[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = load_packet_nt<Tin>(p + (q + u * THREADS) * N);
+        for (int u = 0; u < U; ++u) {
+            const int64_t q = q0 + static_cast<int64_t>(u) * THREADS;
+            raw[u] = q < pe ? load_raw_nt(p + q * N) : splat(kPad);
+        }
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u) {
+            float v[N];
+            unpack<Tin>(raw[u], v);
 #pragma unroll
-            for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v[u].v[j]));
-    }
-    for (; q < pe; q += THREADS) {
-        const Packet<Tin> v = load_packet_nt<Tin>(p + q * N);
-#pragma unroll
-        for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, Elem<Tin>::load(v.v[j]));
+            for (int j = 0; j < N; ++j) acc = Combine<OP>::apply(acc, v[j]);
+        }
     }
     return acc;
 }
 
 // The same share for amax / amin on integer keys (NaN when a NaN wins or the
-// share is empty).
+// share is empty).  The padding is the NaN pattern whose key loses to every
+// value.
 template <typename Tin, int OP, int THREADS>
 __device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, int64_t pb,
                                           int64_t pe, int tid) {
@@ -165,25 +196,26 @@ __device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, 
     constexpr int U = 4;
     using K = KeyOps<OP>;
     constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
+    constexpr uint32_t kPad = K::kMax ? 0xffffffffu : (kWide ? 0x7fffffffu : 0x7fff7fffu);
     int32_t k32 = K::id32();
     short2_t k16 = {K::id16(), K::id16()};
-    auto take = [&](const uint4& raw) {
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (kWide) k32 = K::pick(k32, key32(w[i]));
-            else k16 = K::pick(k16, key16x2(w[i]));
-        }
-    };
-    int64_t q = pb + tid;
-    for (; q + (U - 1) * THREADS < pe; q += U * THREADS) {
+    for (int64_t q0 = pb + tid; q0 < pe; q0 += static_cast<int64_t>(U) * THREADS) {
         uint4 raw[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = load_raw_nt(p + (q + u * THREADS) * N);
+        for (int u = 0; u < U; ++u) {
+            const int64_t q = q0 + static_cast<int64_t>(u) * THREADS;
+            raw[u] = q < pe ? load_raw_nt(p + q * N) : splat(kPad);
+        }
 #pragma unroll
-        for (int u = 0; u < U; ++u) take(raw[u]);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (kWide) k32 = K::pick(k32, key32(w[i]));
+                else k16 = K::pick(k16, key16x2(w[i]));
+            }
+        }
     }
-    for (; q < pe; q += THREADS) take(load_raw_nt(p + q * N));
     if constexpr (kWide) return K::value32(k32);
     else return K::template value16<Tin>(k16);
 }
@@ -222,14 +254,14 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
             }
         }
     }
-    acc = wave_reduce<OP>(acc);
+    acc = lane_reduce<OP>(acc);
     if constexpr (WAVES > 1) {
         __shared__ float partial[kBlock / kWave];
         if (lane == 0) partial[wave] = acc;
         __syncthreads();
         if (wave == 0) {
             acc = lane < WAVES ? partial[lane] : Combine<OP>::identity();
-            acc = wave_reduce<OP>(acc);
+            acc = lane_reduce<OP>(acc);
         }
         if (threadIdx.x == 0 && seg < nsegs) {
             out[seg] = Elem<Tout>::store(finish<OP>(acc, count, final_pass));
@@ -476,7 +508,9 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
             x, partial, outer, r, inner, chunk, nchunk, false, r);
     }
     TP_AMD_HIP_CHECK(hipGetLastError());
-    const bool vec2 = inner % 4 == 0;
+    // The partials are small; spreading their columns over more blocks (one
+    // float per lane) beats 16-byte packets on a few blocks.
+    const bool vec2 = inner % 4 == 0 && inner / (kColLanes * 4) >= cus;
     const int64_t cpb2 = static_cast<int64_t>(kColLanes) * (vec2 ? 4 : 1);
     const dim3 grid2(static_cast<unsigned>((inner + cpb2 - 1) / cpb2), 1u,
                      static_cast<unsigned>(z));
