@@ -47,6 +47,25 @@ void tp_mlu_empty_cache(void);
  * the calling thread's last error message ("" when none). */
 const char* tp_mlu_last_error(void);
 
+/* ---- recording and replay (GraphCapture.cpp:38-130) --------------------- */
+
+/* Replace tp_mlu_capture_* (GraphCapture.cpp:59-129, bound at
+ * tensorplay_mlu/__init__.py:81-92), one recording per process, on a
+ * device's stream as a HIP graph.  begin drains the stream and starts
+ * recording; end stops it, sets aside the blocks handed out meanwhile and
+ * instantiates the graph (an error when the recorded step did host work);
+ * invoke queues one replay; reset drops the recording and returns its
+ * blocks.  Return 0, or -1 with the message in tp_mlu_last_error. */
+int tp_mlu_capture_begin(int index);
+int tp_mlu_capture_end(int index);
+int tp_mlu_capture_invoke(int index);
+int tp_mlu_capture_reset(void);
+/* 1 when a recording is held and can be invoked (GraphCapture.cpp:62). */
+int tp_mlu_capture_ready(void);
+/* out[0]: blocks handed out while the last recording ran; out[1]: blocks
+ * set aside for recordings (GraphCapture.cpp:65-68). */
+void tp_mlu_capture_stats(int64_t* out);
+
 /* ---- device hooks (MLUHooks.cpp:14-52, MLURuntime.cpp:43-136) ---------- */
 
 /* PrivateUse1HooksInterface::is_available (MLUHooks.cpp:15). */

@@ -69,6 +69,12 @@ PROTOTYPES = {
     "tp_mlu_reset_peak_memory_stats": (None, [i32]),
     "tp_mlu_empty_cache": (None, []),
     "tp_mlu_last_error": (C.c_char_p, []),
+    "tp_mlu_capture_begin": (i32, [i32]),
+    "tp_mlu_capture_end": (i32, [i32]),
+    "tp_mlu_capture_invoke": (i32, [i32]),
+    "tp_mlu_capture_reset": (i32, []),
+    "tp_mlu_capture_ready": (i32, []),
+    "tp_mlu_capture_stats": (None, [I64P]),
     "tp_amd_is_available": (i32, []),
     "tp_amd_current_device": (i32, [C.POINTER(C.c_int)]),
     "tp_amd_set_device": (i32, [i32]),

@@ -55,6 +55,12 @@ void reset_peak_memory_stats(int device) { instance().reset_peak(resolve_device(
 
 void empty_cache() { instance().empty_cache(device_count()); }
 
+void set_capture_holding(bool on) { instance().set_capture_holding(on); }
+void freeze_capture_blocks() { instance().freeze_capture_blocks(); }
+void drop_capture_blocks() { instance().drop_capture_blocks(device_count()); }
+int64_t capture_allocations() { return instance().capture_allocations(); }
+int64_t capture_blocks() { return instance().capture_blocks(); }
+
 }  // namespace tp_amd
 
 using namespace tp_amd;

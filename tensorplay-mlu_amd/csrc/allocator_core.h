@@ -23,6 +23,7 @@
 #include <cstdint>
 #include <map>
 #include <mutex>
+#include <vector>
 #include <string>
 
 namespace tp_amd {
@@ -57,6 +58,9 @@ struct Block {
     void* ptr;
     size_t size;
     int device;
+    // Handed out while recording number ``recorded`` (0: none) of device
+    // work ran: that recording may read or write it on every replay.
+    uint64_t recorded = 0;
 };
 
 template <int MaxDevices>
@@ -76,7 +80,7 @@ public:
             Block* block = it->second;
             pool.free_blocks.erase(it);
             note_allocated(pool, block->size);
-            return block;
+            return note_recorded(block);
         }
         void* ptr = backend_.allocate(device, size, backend_.state);
         if (ptr == nullptr) {
@@ -94,15 +98,76 @@ public:
         pool.stats.peak_reserved = std::max(pool.stats.peak_reserved, pool.stats.reserved);
         Block* block = new Block{ptr, size, device};
         note_allocated(pool, size);
-        return block;
+        return note_recorded(block);
     }
 
+    // A block whose last user is gone.  One handed out during a recording
+    // that has ended is set aside instead: the recording still touches it on
+    // every replay.  While the recording runs it may be reused, because the
+    // recorded work keeps its order.
     void give_back(Block* block) {
         if (block == nullptr) return;
         std::lock_guard<std::mutex> lock(mutex_);
         Pool& pool = pools_.at(block->device);
         pool.stats.allocated -= static_cast<int64_t>(block->size);
+        if (block->recorded == generation_ && !holding_) {
+            held_.push_back(block);
+            return;
+        }
         pool.free_blocks.emplace(block->size, block);
+    }
+
+    // ---- recording support (the reference's MLUAllocator.cpp:144-201) ----
+
+    // Start (on) or stop marking the blocks handed out.
+    void set_capture_holding(bool on) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        if (on) capture_allocations_ = 0;
+        holding_ = on;
+    }
+
+    // At the end of a recording: the recorded blocks sitting free in the
+    // pools leave them, so nothing else is handed memory the replays use.
+    void freeze_capture_blocks() {
+        std::lock_guard<std::mutex> lock(mutex_);
+        for (Pool& pool : pools_) {
+            for (auto it = pool.free_blocks.begin(); it != pool.free_blocks.end();) {
+                if (it->second->recorded == generation_) {
+                    held_.push_back(it->second);
+                    it = pool.free_blocks.erase(it);
+                } else {
+                    ++it;
+                }
+            }
+        }
+    }
+
+    // After the recording is dropped: the blocks set aside go back to the
+    // backend (once the devices [0, ndevices) are idle), and blocks of that
+    // recording still in use return to the pool as usual when freed.
+    void drop_capture_blocks(int ndevices) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        ++generation_;
+        if (held_.empty()) return;
+        for (int d = 0; d < ndevices && d < MaxDevices; ++d) backend_.wait(d, backend_.state);
+        for (Block* block : held_) {
+            backend_.release(block->device, block->ptr, backend_.state);
+            pools_.at(block->device).stats.reserved -= static_cast<int64_t>(block->size);
+            delete block;
+        }
+        held_.clear();
+    }
+
+    // Blocks handed out since the last set_capture_holding(true).
+    int64_t capture_allocations() {
+        std::lock_guard<std::mutex> lock(mutex_);
+        return capture_allocations_;
+    }
+
+    // Blocks set aside for a recording.
+    int64_t capture_blocks() {
+        std::lock_guard<std::mutex> lock(mutex_);
+        return static_cast<int64_t>(held_.size());
     }
 
     MemoryStats stats(int device) {
@@ -134,6 +199,15 @@ private:
         MemoryStats stats;
     };
 
+    // Caller holds mutex_.
+    Block* note_recorded(Block* block) {
+        if (holding_) {
+            block->recorded = generation_;
+            ++capture_allocations_;
+        }
+        return block;
+    }
+
     static void note_allocated(Pool& pool, size_t size) {
         pool.stats.allocated += static_cast<int64_t>(size);
         pool.stats.peak_allocated = std::max(pool.stats.peak_allocated, pool.stats.allocated);
@@ -156,6 +230,10 @@ private:
     AllocatorBackend backend_;
     std::mutex mutex_;
     std::array<Pool, MaxDevices> pools_;
+    bool holding_ = false;
+    uint64_t generation_ = 1;  // number of the current (or next) recording
+    int64_t capture_allocations_ = 0;
+    std::vector<Block*> held_;
 };
 
 }  // namespace tp_amd

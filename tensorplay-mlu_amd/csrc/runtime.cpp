@@ -98,8 +98,24 @@ hipStream_t stream(int index) {
     return s;
 }
 
+namespace {
+
+// Host copies and synchronisation cannot be part of a recorded sequence
+// (the recording holds device work only): refuse them while the stream is
+// being recorded, before anything reaches the runtime.
+void refuse_while_recording(hipStream_t s, const char* what) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    TP_AMD_HIP_CHECK(hipStreamIsCapturing(s, &status));
+    TP_AMD_CHECK(status == hipStreamCaptureStatusNone, what,
+                 " while the stream is being recorded: a recorded step may only queue "
+                 "device work");
+}
+
+}  // namespace
+
 void synchronize(int index) {
     DeviceGuard guard(index);
+    refuse_while_recording(stream(index), "synchronisation");
     TP_AMD_HIP_CHECK(hipStreamSynchronize(stream(index)));
 }
 
@@ -107,6 +123,7 @@ void copy_to_device(void* device_dst, const void* host_src, size_t nbytes, int i
     if (nbytes == 0) return;
     DeviceGuard guard(index);
     hipStream_t s = stream(index);
+    refuse_while_recording(s, "a host-to-device copy");
     TP_AMD_HIP_CHECK(hipMemcpyAsync(device_dst, host_src, nbytes, hipMemcpyHostToDevice, s));
     TP_AMD_HIP_CHECK(hipStreamSynchronize(s));
 }
@@ -115,6 +132,7 @@ void copy_to_host(void* host_dst, const void* device_src, size_t nbytes, int ind
     if (nbytes == 0) return;
     DeviceGuard guard(index);
     hipStream_t s = stream(index);
+    refuse_while_recording(s, "a device-to-host copy");
     TP_AMD_HIP_CHECK(hipMemcpyAsync(host_dst, device_src, nbytes, hipMemcpyDeviceToHost, s));
     TP_AMD_HIP_CHECK(hipStreamSynchronize(s));
 }

@@ -84,6 +84,14 @@ void shim_reset_peak(int dev) { g_core->reset_peak(dev); }
 void shim_empty(void) { g_core->empty_cache(4); }
 size_t shim_cached(int dev) { return g_core->cached_blocks(dev); }
 
+void shim_capture_holding(int on) { g_core->set_capture_holding(on != 0); }
+void shim_freeze(void) { g_core->freeze_capture_blocks(); }
+void shim_drop(void) { g_core->drop_capture_blocks(4); }
+void shim_capture_stats(long long* out) {
+    out[0] = g_core->capture_allocations();
+    out[1] = g_core->capture_blocks();
+}
+
 void shim_counts(long* out) {
     out[0] = g_state.allocs;
     out[1] = g_state.frees;

@@ -35,6 +35,8 @@ def shim(tmp_path_factory):
     lib.shim_cached.restype = C.c_size_t
     lib.shim_counts.argtypes = [C.POINTER(C.c_long)]
     lib.shim_reset_peak.argtypes = [C.c_int]
+    lib.shim_capture_holding.argtypes = [C.c_int]
+    lib.shim_capture_stats.argtypes = [C.POINTER(C.c_longlong)]
     return lib
 
 
@@ -122,3 +124,51 @@ def test_out_of_memory_releases_the_cache_and_retries_once(shim):
     assert stats(shim)[0] == 20 * MiB
     shim.shim_give(b)
     shim.shim_give(c)
+
+
+def capture_stats(shim):
+    out = (C.c_longlong * 2)()
+    shim.shim_capture_stats(out)
+    return out[0], out[1]
+
+
+def test_recording_sets_blocks_aside(shim):
+    """Blocks handed out while a sequence is recorded are reused during the
+    recording, set aside once it ends, and returned when it is dropped
+    (the reference's MLUAllocator.cpp:130-201)."""
+    shim.shim_reset(1 << 30)
+    plain = shim.shim_take(0, 1 * MiB)           # before the recording
+    shim.shim_capture_holding(1)
+    a = shim.shim_take(0, 4 * MiB)
+    a_ptr = shim.shim_block_ptr(a)
+    shim.shim_give(a)                            # freed inside the recording ...
+    b = shim.shim_take(0, 4 * MiB)               # ... may be reused inside it
+    assert shim.shim_block_ptr(b) == a_ptr
+    c = shim.shim_take(0, 8 * MiB)
+    shim.shim_give(c)                            # free at the end of the recording
+    shim.shim_capture_holding(0)
+    shim.shim_freeze()
+    assert capture_stats(shim) == (3, 1)         # three hand-outs; c set aside
+    assert shim.shim_cached(0) == 0
+    shim.shim_give(b)                            # a recorded block freed afterwards
+    assert capture_stats(shim)[1] == 2
+    d = shim.shim_take(0, 4 * MiB)               # is not handed out again
+    assert shim.shim_block_ptr(d) != a_ptr
+    shim.shim_give(d)
+    shim.shim_give(plain)
+    assert shim.shim_cached(0) == 2              # unrecorded blocks stay cached
+    reserved_before = stats(shim, 0)[1]
+    waits_before = counts(shim)[2]
+    shim.shim_drop()
+    assert capture_stats(shim)[1] == 0
+    assert stats(shim, 0)[1] == reserved_before - 12 * MiB
+    assert counts(shim)[2] > waits_before        # the device was drained first
+    # a block of the dropped recording freed afterwards returns to the pool
+    shim.shim_capture_holding(1)
+    e = shim.shim_take(0, 2 * MiB)
+    shim.shim_capture_holding(0)
+    shim.shim_freeze()
+    shim.shim_drop()
+    cached = shim.shim_cached(0)
+    shim.shim_give(e)
+    assert capture_stats(shim)[1] == 0 and shim.shim_cached(0) == cached + 1
