@@ -9,20 +9,29 @@
 //     LDS read gives a lane 4 consecutive k that feed 4 back-to-back MFMAs
 //     (lane half h supplies k = 4h + j to MFMA j, for A and B alike, so the
 //     pairing of A and B elements is exact whatever order the sum takes).
-// Two block shapes: 256 x 256 with 8 waves (2 x 4, each wave a 128 x 64
-// patch of 4 x 2 MFMA tiles of 32 x 32) for large problems, and 128 x 128
-// with 4 waves (2 x 2, each 64 x 64) when the big tiles would leave CUs idle.
-// K advances BK at a time through two LDS stages: while the waves multiply
-// out of one stage, the next K tile is written into the other and the one
-// after is already in flight from global memory, so each K step needs a
-// single barrier.  Operands sit in LDS K-major ([row][k], rows padded by 16
-// bytes so the 16-byte fragment reads of 16 consecutive rows hit distinct
-// banks).  An operand stored K-major in memory is copied with 16-byte loads;
-// one stored with its M (or N) axis contiguous -- a transposed view, read in
-// place -- is loaded as V x 4 blocks (V along M/N, 4 along K) and transposed
-// in registers before its LDS store.  Tiles are numbered so each of the 8
+// Three kernels, tried in this order:
+//   * 16-bit operands, M and N multiples of 256, K of 128, at least one
+//     256 x 256 tile per CU: `big` below -- four waves of 128 x 128, operand
+//     tiles loaded straight into LDS by buffer loads and read back with
+//     ds_read_b128 (K-major operands) or ds_read_b64_tr_b16 (transposed
+//     views, read in place); no bounds checks anywhere in the K loop.
+//   * other 16-bit products with a 256 x 256 tile per CU: 256 x 256 with
+//     8 waves (2 x 4, each wave a 128 x 64 patch of 4 x 2 MFMA tiles of
+//     32 x 32).
+//   * everything else: 128 x 128 with 4 waves (2 x 2, each 64 x 64).
+// The last two advance K BK at a time through two LDS stages: while the
+// waves multiply out of one stage, the next K tile is written into the
+// other and the one after is already in flight from global memory, so each
+// K step needs a single barrier.  Operands sit in LDS K-major ([row][k],
+// rows padded by 16 bytes so the 16-byte fragment reads of 16 consecutive
+// rows hit distinct banks).  An operand stored K-major in memory is copied
+// with 16-byte loads; one stored with its M (or N) axis contiguous is loaded
+// as V x 4 blocks (V along M/N, 4 along K) and transposed in registers
+// before its LDS store.  All kernels number their tiles so each of the 8
 // XCDs walks a contiguous range in groups of 8 tile rows, keeping an XCD's A
 // and B panels hot in its own L2.
+
+#include <type_traits>
 
 #include "device_common.h"
 #include "gemm.h"
@@ -353,6 +362,308 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
     }
 }
 
+namespace big {
+
+// 256 x 256 x 64 tiles, four waves of 128 x 128, every tile full.
+//
+// Operand tiles move from memory straight into LDS with buffer loads (16
+// bytes a lane, no registers in between).  Each operand tile is 32 KB in one
+// of two layouts:
+//   * K-major operand: 256 rows (M or N) of 128 bytes, one row = the tile's
+//     64 k; logical 16-byte chunk c of row r sits at slot c ^ (r & 7).  A
+//     load instruction fills 8 rows; a fragment read (ds_read_b128: 32 rows,
+//     one chunk) then touches every bank once per 8 lanes.
+//   * M/N-major operand (a transposed view, read in place): 64 rows (k) of
+//     512 bytes, chunk c of row k at slot c ^ 2 (k & 3).  A load instruction
+//     fills 2 rows.  Fragments come from ds_read_b64_tr_b16, which hands
+//     each lane of a 16-lane group one column of a 4 x 16 block: two of them
+//     give a lane its 8 consecutive k; the four rows a group reads fall in
+//     distinct banks.
+// The loads for K tile kt + 1 go out during the first half of step kt into
+// the other LDS stage, interleaved with the MFMAs.
+constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
+constexpr int TILE = 256 * 128;   // bytes per operand tile
+constexpr int STAGE = 2 * TILE;   // bytes per LDS stage
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
+                                             0x00020000);
+}
+
+// One operand: the block's 256-wide panel of X (M or N from mn0) and how
+// its tiles reach LDS and registers.
+template <bool KMAJOR>
+struct Operand {
+    __amdgpu_buffer_rsrc_t res;
+    uint32_t voff;     // per-lane byte offset of a load
+    uint32_t sbase;    // this wave's first load, bytes
+    uint32_t sstep;    // between a wave's successive loads, bytes
+    uint32_t kstep;    // per K tile, bytes
+    int frag[4];       // per-lane fragment byte offsets (K-major: per substep; M/N-major: per tile)
+
+    __device__ __forceinline__ void init(const void* X, int64_t ld, int64_t mn0, int64_t K, int wave,
+                                         int lane, int wbase) {
+        const int l32 = lane % 32, half = lane / 32;
+        if constexpr (KMAJOR) {
+            // element (r, k) at X[r * ld + k]
+            res = rsrc(static_cast<const uint16_t*>(X) + mn0 * ld, static_cast<uint32_t>(256 * ld * 2));
+            const int row = lane >> 3, chunk = (lane & 7) ^ row;
+            voff = static_cast<uint32_t>((row * ld + chunk * 8) * 2);
+            sbase = static_cast<uint32_t>(wave * 8 * ld * 2);  // row groups wave, wave + 4, ...
+            sstep = static_cast<uint32_t>(32 * ld * 2);
+            kstep = BK * 2;
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                frag[s] = (wbase + l32) * 128 + ((((2 * s + half) ^ (l32 & 7))) << 4);
+        } else {
+            // element (k, r) at X[k * ld + r]
+            res = rsrc(static_cast<const uint16_t*>(X) + mn0, static_cast<uint32_t>(K * ld * 2));
+            const int row = lane >> 5;                       // of the instruction's 2 rows
+            const int chunk = (lane & 31) ^ (2 * ((2 * (wave & 1) + row) & 3));
+            voff = static_cast<uint32_t>((row * ld + chunk * 8) * 2);
+            sbase = static_cast<uint32_t>(2 * wave * ld * 2);  // row pairs wave, wave + 4, ...
+            sstep = static_cast<uint32_t>(8 * ld * 2);
+            kstep = static_cast<uint32_t>(BK * ld * 2);
+            // Transposed reads: lane p of 16-lane group g addresses row
+            // 8 * half + p / 4 (+ 16 s + 4 h) and column 16 (g & 1) + 4 (p % 4)
+            // of the wave's 32-wide tile t.
+            const int g = lane / 16, pl = lane % 16;
+            const int krow = 8 * half + pl / 4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int col = wbase + t * 32 + 16 * (g & 1) + 4 * (pl % 4);
+                frag[t] = krow * 512 + (((col / 8) ^ (2 * (krow & 3))) << 4) + (col % 8) * 2;
+            }
+        }
+    }
+
+    // Loads of K tile kt into `tile` (this wave's 8 of the 32 instructions).
+    __device__ __forceinline__ void issue(int kt, char* tile, int wave) const {
+        const uint32_t kb = static_cast<uint32_t>(kt) * kstep;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (lds_ptr)(tile + (i * 4 + wave) * 1024), 16, voff,
+                                                     sbase + i * sstep + kb, 0, 0);
+        }
+    }
+
+    // The 8 k of substep s for the wave's 32-wide tile t.
+    __device__ __forceinline__ uint4 read(const char* tile, int t, int s) const {
+        if constexpr (KMAJOR) {
+            return *reinterpret_cast<const uint4*>(tile + t * 32 * 128 + frag[s]);
+        } else {
+            const char* q = tile + frag[t] + s * 16 * 512;
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(q));
+            const short4_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(q + 4 * 512));
+            uint4 v;
+            __builtin_memcpy(&v, &lo, 8);
+            __builtin_memcpy(reinterpret_cast<char*>(&v) + 8, &hi, 8);
+            return v;
+        }
+    }
+};
+
+template <typename T, bool A_KMAJOR, bool B_KMAJOR>
+__global__ __launch_bounds__(THREADS, 1) void gemm_big_kernel(GemmArgs p) {
+    using S = typename Elem<T>::storage;
+    static_assert(sizeof(S) == 2, "16-bit operands");
+    // Two LDS objects rather than one array: the compiler can then tell that
+    // the loads filling one stage do not touch the stage being read, and
+    // leaves them in flight across the step.
+    __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+
+    const int grid_m = static_cast<int>(p.m / BM), grid_n = static_cast<int>(p.n / BN);
+    int pm, pn;
+    tile_coords(blockIdx.x, grid_m, grid_n, pm, pn);
+    const int64_t m0 = static_cast<int64_t>(pm) * BM, n0 = static_cast<int64_t>(pn) * BN;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int wm = wave / 2, wn = wave % 2;
+    const int l32 = lane % 32, half = lane / 32;
+    const int nk = static_cast<int>(p.k / BK);
+    const int64_t bi = blockIdx.z;
+
+    Operand<A_KMAJOR> oa;
+    Operand<B_KMAJOR> ob;
+    oa.init(static_cast<const S*>(p.a) + bi * p.stride_a, p.lda, m0, p.k, wave, lane, wm * 128);
+    ob.init(static_cast<const S*>(p.b) + bi * p.stride_b, p.ldb, n0, p.k, wave, lane, wn * 128);
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    uint4 af[2][4], bf[2][4];
+    auto fetch = [&](const char* stage, int s, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[buf][i] = oa.read(stage, i, s);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[buf][j] = ob.read(stage + TILE, j, s);
+    };
+    auto mma = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::mma(af[buf][i], bf[buf][j], acc[i][j]);
+    };
+    // Fragment reads per substep: a b128 for a K-major operand, two
+    // transposed b64 for an M/N-major one.
+    constexpr int kReads = 4 * (A_KMAJOR ? 1 : 2) + 4 * (B_KMAJOR ? 1 : 2);
+    auto interleave_reads = [&]() {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (q < kReads) __builtin_amdgcn_sched_group_barrier(0x100, kReads > 16 && q < kReads - 16 ? 2 : 1, 0);
+        }
+    };
+    // One K step out of `cur`, entered with substep 0's fragments in
+    // flight.  Substeps 0-2 each run 16 MFMAs interleaved with the next
+    // substep's fragment reads (and, in substeps 0 and 1, the 8 loads of A
+    // and then of B for the next K tile).  The step then waits for its loads
+    // and the barrier, and starts reading the next step's first fragments
+    // before running substep 3's MFMAs, whose operands are in registers.
+    auto body = [&](const char* cur, char* next, int kt_next, auto do_issue, auto has_next) {
+        constexpr bool kIssue = decltype(do_issue)::value;
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            fetch(cur, s + 1, (s + 1) & 1);
+            if constexpr (kIssue) {
+                if (s == 0) oa.issue(kt_next, next, wave);
+                if (s == 1) ob.issue(kt_next, next + TILE, wave);
+            }
+            mma(s & 1);
+            if (kIssue && s < 2) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, kReads / 8, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            } else {
+                interleave_reads();
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (decltype(has_next)::value) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            fetch(next, 0, 0);
+            mma(1);
+            interleave_reads();
+        } else {
+            mma(1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    oa.issue(0, lds0, wave);
+    ob.issue(0, lds0 + TILE, wave);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    fetch(lds0, 0, 0);
+    // Steps in pairs (stage 0 then stage 1), so every access names its LDS
+    // object statically; the host guarantees an even number of K tiles.
+    for (int kt = 0; kt + 2 < nk; kt += 2) {
+        body(lds0, lds1, kt + 1, std::true_type{}, std::true_type{});
+        body(lds1, lds0, kt + 2, std::true_type{}, std::true_type{});
+    }
+    body(lds0, lds1, nk - 1, std::true_type{}, std::true_type{});
+    body(lds1, lds0, 0, std::false_type{}, std::false_type{});
+
+    // Epilogue: lane holds column l32 of each 32 x 32 tile, rows
+    // 8 * (e / 4) + 4 * half + e % 4 for accumulator element e.
+    S* C = static_cast<S*>(p.c) + bi * p.stride_c;
+    const S* Cin = static_cast<const S*>(p.cin);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t col = n0 + wn * 128 + j * 32 + l32;
+            const int64_t rbase = m0 + wm * 128 + i * 32 + 4 * half;
+            S* cp = C + rbase * p.ldc + col;
+            if (p.beta == 0.0f) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cp[r * p.ldc] = Elem<T>::store(p.alpha * acc[i][j][4 * g + r]);
+                    cp += 8 * p.ldc;
+                }
+            } else if (p.cin_rs == 0) {
+                const float c = p.beta * Elem<T>::load(Cin[bi * p.cin_stride_b + col * p.cin_cs]);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cp[r * p.ldc] = Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c));
+                    cp += 8 * p.ldc;
+                }
+            } else {
+                const S* ci = Cin + bi * p.cin_stride_b + rbase * p.cin_rs + col * p.cin_cs;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float c = Elem<T>::load(ci[r * p.cin_rs]);
+                        cp[r * p.ldc] = Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r]));
+                    }
+                    cp += 8 * p.ldc;
+                    ci += 8 * p.cin_rs;
+                }
+            }
+        }
+}
+
+template <typename T>
+bool eligible(const GemmArgs& p, int cus) {
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    // A block addresses its panel through one buffer resource: 256 rows of
+    // ld (K-major, needs ld >= K) or K rows of ld (M/N-major, needs
+    // ld >= 256), under 4 GiB.
+    auto panel_ok = [&](const void* x, int64_t ld, int64_t stride, bool kmajor) {
+        const int64_t bytes = kmajor ? 256 * ld * 2 : p.k * ld * 2;
+        return aligned16(x) && ld % 8 == 0 && stride % 8 == 0 && bytes < (int64_t(1) << 32) &&
+               (kmajor ? ld >= p.k : ld >= 256);
+    };
+    return p.m % BM == 0 && p.n % BN == 0 && p.k % (2 * BK) == 0 &&
+           panel_ok(p.a, p.lda, p.stride_a, a_kmajor) && panel_ok(p.b, p.ldb, p.stride_b, b_kmajor) &&
+           (p.m / BM) * (p.n / BN) * p.batch >= cus && (p.m / BM) * (p.n / BN) < (int64_t(1) << 31);
+}
+
+template <typename T>
+void launch(const GemmArgs& whole, hipStream_t stream) {
+    constexpr int64_t kMaxZ = 65535;
+    using S = typename Elem<T>::storage;
+    const bool a_kmajor = !whole.trans_a, b_kmajor = whole.trans_b;
+    for (int64_t b0 = 0; b0 < whole.batch; b0 += kMaxZ) {
+        GemmArgs p = whole;
+        p.batch = whole.batch - b0 < kMaxZ ? whole.batch - b0 : kMaxZ;
+        p.a = static_cast<const S*>(whole.a) + b0 * whole.stride_a;
+        p.b = static_cast<const S*>(whole.b) + b0 * whole.stride_b;
+        p.c = static_cast<S*>(whole.c) + b0 * whole.stride_c;
+        if (whole.cin != nullptr) p.cin = static_cast<const S*>(whole.cin) + b0 * whole.cin_stride_b;
+        const dim3 grid(static_cast<unsigned>((p.m / BM) * (p.n / BN)), 1u, static_cast<unsigned>(p.batch));
+        if (a_kmajor && b_kmajor) {
+            gemm_big_kernel<T, true, true><<<grid, THREADS, 0, stream>>>(p);
+        } else if (a_kmajor) {
+            gemm_big_kernel<T, true, false><<<grid, THREADS, 0, stream>>>(p);
+        } else if (b_kmajor) {
+            gemm_big_kernel<T, false, true><<<grid, THREADS, 0, stream>>>(p);
+        } else {
+            gemm_big_kernel<T, false, false><<<grid, THREADS, 0, stream>>>(p);
+        }
+        TP_AMD_HIP_CHECK(hipGetLastError());
+    }
+}
+
+}  // namespace big
+
 template <typename T>
 bool mfma_eligible(const GemmArgs& p) {
     constexpr int V = Mfma<T>::V;
@@ -405,6 +716,10 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     if constexpr (sizeof(typename Elem<T>::storage) == 2) {
+        if (big::eligible<T>(p, cu_count(device))) {
+            big::launch<T>(p, stream);
+            return;
+        }
         const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
         if (big_tiles >= cu_count(device)) {
             launch_config<T, 256, 256, 2, 4>(p, stream);

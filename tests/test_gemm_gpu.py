@@ -196,3 +196,49 @@ def test_config5_bmm_bf16(dev, ops, orc):
     b = sample(orc, (64, 128, 512), BF16, 2, 128 ** -0.25)
     got = ops.bmm(dev.from_numpy(a, dtype=BF16), dev.from_numpy(b, dtype=BF16)).numpy()
     check(orc, got, exact(orc, a, b, BF16), BF16, "bmm 64x512x128x512")
+
+
+# ---- the 256 x 256 four-wave kernel through the kernel C-ABI ---------------------
+
+
+def _padded(orc, shape, pad, dtype, seed):
+    """Random values of ``shape`` stored with ``pad`` extra NaN columns: the
+    array returned is the storage, the view of its first columns the
+    operand.  A kernel that reads the padding produces NaNs."""
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * np.float32(0.25)
+    store = np.full(shape[:-1] + (shape[-1] + pad,), np.nan, np.float32)
+    store[..., :shape[-1]] = x
+    return orc.from_float(store, dtype)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("bt,m,n,k", [(256, 256, 256, 256), (64, 512, 512, 320)],
+                         ids=["big-tiles", "K-tail-fallback"])
+def test_gemm_abi_padded_batched(amd, dev, orc, dtype, ta, tb, bt, m, n, k):
+    """tp_amd_launch_gemm on a batch of products with padded leading
+    dimensions (NaN padding), alpha = 0.5 and beta = 2 with a full Cin.  The
+    first shape has one 256 x 256 tile per CU and four K tiles (the
+    four-wave kernel); the second, K = 320, is not a multiple of 128 and
+    takes the eight-wave kernel."""
+    lib = amd.load()
+    pad, alpha, beta = 8, 0.5, 2.0
+    a = _padded(orc, (bt, k, m) if ta else (bt, m, k), pad, dtype, 1)
+    b = _padded(orc, (bt, n, k) if tb else (bt, k, n), pad, dtype, 2)
+    cin = sample(orc, (bt, m, n), dtype, 3)
+    lda, ldb = a.shape[-1], b.shape[-1]
+    da, db, dc = (dev.from_numpy(x, dtype=dtype) for x in (a, b, cin))
+    out = dev.empty((bt, m, n), dtype=dtype)
+    st = lib.tp_amd_launch_gemm(0, dtype, bt, m, n, k, alpha, da.data_ptr, lda, a.shape[-2] * lda,
+                                int(ta), db.data_ptr, ldb, b.shape[-2] * ldb, int(tb), beta,
+                                dc.data_ptr, n, 1, m * n, out.data_ptr, n, m * n)
+    assert st == 0, lib.tp_mlu_last_error()
+    A = orc.to_float(a, dtype)[..., :(m if ta else k)]
+    B = orc.to_float(b, dtype)[..., :(k if tb else n)]
+    A = np.swapaxes(A, -1, -2) if ta else A
+    B = np.swapaxes(B, -1, -2) if tb else B
+    want = alpha * np.matmul(A, B) + beta * orc.to_float(cin, dtype)
+    got = out.numpy()
+    assert not np.isnan(orc.to_float(got, dtype)).any(), "padding leaked into the product"
+    check(orc, got, want, dtype, f"gemm abi {bt}x{m}x{n}x{k} ta={ta} tb={tb}")
