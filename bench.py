@@ -338,7 +338,8 @@ def profile_launches(what: str, lib, ops, dev) -> None:
     traffic: ten launches of a copy-like kernel (affine y = 1 x + 0 on
              [8192, 8192] float32, 2 x 268,435,456 B) to calibrate the
              FETCH_SIZE / WRITE_SIZE counters, then ten of the dominant kernel;
-    gemm:    ten bf16 4096^3 products (A, B row-major);
+    gemm:    ten bf16 4096^3 products in each operand layout (A, B
+             row-major; B transposed; A transposed; both transposed);
     reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
              and bf16, five each."""
     import ctypes as C
@@ -359,10 +360,11 @@ def profile_launches(what: str, lib, ops, dev) -> None:
         a = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
         b = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
         c = ops.empty((K, K), BF16)
-        for _ in range(10):
-            assert lib.tp_amd_launch_gemm(0, BF16, 1, K, K, K, 1.0, a.data_ptr, K, 0, 0,
-                                          b.data_ptr, K, 0, 0, 0.0, None, 0, 0, 0,
-                                          c.data_ptr, K, 0) == 0
+        for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+            for _ in range(10):
+                assert lib.tp_amd_launch_gemm(0, BF16, 1, K, K, K, 1.0, a.data_ptr, K, 0, ta,
+                                              b.data_ptr, K, 0, tb, 0.0, None, 0, 0, 0,
+                                              c.data_ptr, K, 0) == 0
     elif what == "reduce":
         g = np.random.default_rng(0)
         x32 = dev.from_numpy(g.standard_normal((32768, 4096), dtype=np.float32))
