@@ -271,13 +271,12 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
     }
 }
 
-// amax / amin of one thread's N columns over rows row0, row0 + 4, ... < end
+// amax / amin of one thread's N columns over rows row0, row0 + G, ... < end
 // on integer keys (a column comes out NaN when a NaN wins or it has no rows).
-template <typename Tin, int OP>
+template <typename Tin, int OP, int G, bool NT>
 __device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
                                           const typename Elem<Tin>::storage* p, int64_t row0,
                                           int64_t end, int64_t inner) {
-    constexpr int G = kBlock / 64;  // row groups
     constexpr int U = 8;
     using K = KeyOps<OP>;
     constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
@@ -300,11 +299,14 @@ __device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
     for (; row + (U - 1) * G < end; row += U * G) {
         uint4 raw[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = load_raw_nt(p + (row + u * G) * inner);
+        for (int u = 0; u < U; ++u) {
+            const auto* q = p + (row + u * G) * inner;
+            raw[u] = NT ? load_raw_nt(q) : *reinterpret_cast<const uint4*>(q);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) take(raw[u]);
     }
-    for (; row < end; row += G) take(load_raw_nt(p + row * inner));
+    for (; row < end; row += G) take(*reinterpret_cast<const uint4*>(p + row * inner));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         if constexpr (kWide) {
@@ -316,20 +318,47 @@ __device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
     }
 }
 
-// Column chunks.  Block (bx, ch, z): columns [bx * 64 * N, +64 * N) of every
-// outer index o = z, z + gridDim.z, ...; rows [ch * chunk, +chunk) split
-// over 4 row groups.  Writes out[(o * nchunk + ch) * inner + col].
-constexpr int kColLanes = 64;
-constexpr int kRowGroups = kBlock / kColLanes;
+// Column reductions.  A block covers the columns of col_lanes lanes (16
+// lanes of 16-byte packets of a 16-bit type, 64 lanes of float32 packets or
+// of single elements) over the rows [ch * chunk, +chunk) of every outer index
+// o = z, z + gridDim.z, ...; its kBlock / col_lanes row groups stride down
+// those rows, and the groups are combined in a fixed order.  With one chunk
+// the block writes the result; otherwise it writes float32 partials
+// out[(o * nchunk + ch) * inner + col].
+//
+// FUSE folds the second pass in: the partials are written and read back
+// with agent-coherent accesses; every block counts its arrival in
+// col_counters[o * gridDim.x + blockIdx.x] once its partial stores have
+// completed, and the last of the nchunk blocks of a column range reads the
+// nchunk partials back in chunk order, writes the result, and resets the
+// counter to zero for the next launch.  The counters start at zero (device
+// globals are zeroed when the code object loads).
+template <typename Tin, bool VEC>
+constexpr int col_lanes() {
+    // Measured on X1 and X2 of config 3: 16-bit packets run best as 16 lanes
+    // (128 columns) per row, float32 packets and single elements as 64.
+    return VEC && sizeof(typename Elem<Tin>::storage) == 2 ? 16 : 64;
+}
 
-template <typename Tin, typename Tout, int OP, bool VEC>
+constexpr int64_t kMaxColCounters = 8192;
+__device__ unsigned int col_counters[kMaxColCounters];
+
+template <typename Tin, typename Tout, int OP, bool VEC, bool FUSE>
 __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
-    const typename Elem<Tin>::storage* x, typename Elem<Tout>::storage* out, int64_t outer,
-    int64_t r, int64_t inner, int64_t chunk, int64_t nchunk, bool final_pass, int64_t count) {
+    const typename Elem<Tin>::storage* x, typename Elem<Tout>::storage* out,
+    typename Elem<Tin>::storage* result, int64_t outer, int64_t r, int64_t inner, int64_t chunk,
+    int64_t nchunk, bool final_pass, int64_t count) {
     constexpr int N = VEC ? Packet<Tin>::N : 1;
-    __shared__ float partial[kRowGroups][kColLanes * N + 1];
-    const int lane = threadIdx.x % kColLanes, rg = threadIdx.x / kColLanes;
-    const int64_t col = (static_cast<int64_t>(blockIdx.x) * kColLanes + lane) * N;
+    constexpr int LANES = col_lanes<Tin, VEC>();
+    // Non-temporal loads measured faster with 64 lanes a row, plain ones
+    // with 16.
+    constexpr bool NT = LANES == 64;
+    constexpr int G = kBlock / LANES;  // row groups
+    constexpr int COLS = LANES * N;    // columns per block
+    __shared__ float partial[G][COLS + 1];
+    __shared__ bool last;
+    const int lane = threadIdx.x % LANES, rg = threadIdx.x / LANES;
+    const int64_t col = (static_cast<int64_t>(blockIdx.x) * LANES + lane) * N;
     const int64_t ch = blockIdx.y;
     const int64_t begin = ch * chunk;
     const int64_t end = begin + chunk < r ? begin + chunk : r;
@@ -340,7 +369,7 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
         bool exact = !(kMinMax<OP> && VEC);
         if constexpr (kMinMax<OP> && VEC) {
             if (col < inner) {
-                cols_keys<Tin, OP>(acc, x + o * r * inner + col, begin + rg, end, inner);
+                cols_keys<Tin, OP, G, NT>(acc, x + o * r * inner + col, begin + rg, end, inner);
 #pragma unroll
                 for (int j = 0; j < N; ++j) exact = exact || acc[j] != acc[j];
                 if (exact) {
@@ -353,12 +382,14 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
             const typename Elem<Tin>::storage* p = x + o * r * inner + col;
             int64_t row = begin + rg;
             constexpr int U = 8;
-            for (; row + (U - 1) * kRowGroups < end; row += U * kRowGroups) {
+            for (; row + (U - 1) * G < end; row += U * G) {
                 if constexpr (VEC) {
                     Packet<Tin> v[U];
 #pragma unroll
-                    for (int u = 0; u < U; ++u)
-                        v[u] = load_packet_nt<Tin>(p + (row + u * kRowGroups) * inner);
+                    for (int u = 0; u < U; ++u) {
+                        const auto* q = p + (row + u * G) * inner;
+                        v[u] = NT ? load_packet_nt<Tin>(q) : load_packet<Tin>(q);
+                    }
 #pragma unroll
                     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -367,15 +398,15 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
                 } else {
                     typename Elem<Tin>::storage v[U];
 #pragma unroll
-                    for (int u = 0; u < U; ++u) v[u] = p[(row + u * kRowGroups) * inner];
+                    for (int u = 0; u < U; ++u) v[u] = p[(row + u * G) * inner];
 #pragma unroll
                     for (int u = 0; u < U; ++u)
                         acc[0] = Combine<OP>::apply(acc[0], Elem<Tin>::load(v[u]));
                 }
             }
-            for (; row < end; row += kRowGroups) {
+            for (; row < end; row += G) {
                 if constexpr (VEC) {
-                    const Packet<Tin> v = load_packet_nt<Tin>(p + row * inner);
+                    const Packet<Tin> v = load_packet<Tin>(p + row * inner);
 #pragma unroll
                     for (int j = 0; j < N; ++j)
                         acc[j] = Combine<OP>::apply(acc[j], Elem<Tin>::load(v.v[j]));
@@ -387,15 +418,61 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
 #pragma unroll
         for (int j = 0; j < N; ++j) partial[rg][lane * N + j] = acc[j];
         __syncthreads();
-        // Row group 0 combines the four groups in a fixed order.
-        for (int e = threadIdx.x; e < kColLanes * N; e += kBlock) {
+        // The row groups are combined in a fixed order.
+        for (int e = threadIdx.x; e < COLS; e += kBlock) {
             float v = partial[0][e];
 #pragma unroll
-            for (int g = 1; g < kRowGroups; ++g) v = Combine<OP>::apply(v, partial[g][e]);
-            const int64_t c = static_cast<int64_t>(blockIdx.x) * kColLanes * N + e;
+            for (int g = 1; g < G; ++g) v = Combine<OP>::apply(v, partial[g][e]);
+            const int64_t c = static_cast<int64_t>(blockIdx.x) * COLS + e;
             if (c < inner) {
-                out[(o * nchunk + ch) * inner + c] =
-                    Elem<Tout>::store(finish<OP>(v, count, final_pass));
+                auto* dst = out + (o * nchunk + ch) * inner + c;
+                const auto val = Elem<Tout>::store(finish<OP>(v, count, final_pass));
+                if constexpr (FUSE) {
+                    // Agent-coherent store: written through past this XCD's L2.
+                    __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    *dst = val;
+                }
+            }
+        }
+        if constexpr (FUSE) {
+            static_assert(std::is_same<Tout, float>::value, "partials are float32");
+            // Every thread's partial stores have completed (device-visible,
+            // being agent-coherent) before the block counts its arrival.  A
+            // device-scope fence would write back the whole L2 per block.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            const int64_t slot = o * gridDim.x + blockIdx.x;
+            if (threadIdx.x == 0) {
+                last = __hip_atomic_fetch_add(&col_counters[slot], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT) == nchunk - 1;
+            }
+            __syncthreads();
+            if (last) {
+                for (int e = threadIdx.x; e < COLS; e += kBlock) {
+                    const int64_t c = static_cast<int64_t>(blockIdx.x) * COLS + e;
+                    if (c < inner) {
+                        float* q = out + o * nchunk * inner + c;
+                        auto at = [&](int64_t k) {
+                            return __hip_atomic_load(q + k * inner, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        };
+                        // Eight loads in flight at a time, folded in chunk order.
+                        float v = at(0);
+                        int64_t k = 1;
+                        for (; k + 8 <= nchunk; k += 8) {
+                            float t[8];
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) t[u] = at(k + u);
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) v = Combine<OP>::apply(v, t[u]);
+                        }
+                        for (; k < nchunk; ++k) v = Combine<OP>::apply(v, at(k));
+                        result[o * inner + c] = Elem<Tin>::store(finish<OP>(v, count, true));
+                    }
+                }
+                if (threadIdx.x == 0) {
+                    __hip_atomic_store(&col_counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
         __syncthreads();
@@ -469,12 +546,12 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     }
     // Column reductions.
     const bool vec = inner % N == 0 && aligned16(x);
-    const int64_t cols_per_block = static_cast<int64_t>(kColLanes) * (vec ? N : 1);
+    const int64_t cols_per_block = vec ? col_lanes<T, true>() * N : col_lanes<T, false>();
     const int64_t bx = (inner + cols_per_block - 1) / cols_per_block;
     const int64_t z = outer < 65535 ? outer : 65535;
     const int64_t base_blocks = bx * z;
     // Two blocks per CU, each with eight 16-byte loads per thread in flight,
-    // keep HBM busy; more chunks would only grow the second pass.
+    // keep HBM busy; more chunks would only grow the partials.
     const int64_t target_blocks = cus * 2;
     int64_t nchunk = 1;
     if (base_blocks < target_blocks && r >= 64) {
@@ -489,37 +566,28 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
                     static_cast<unsigned>(z));
     if (nchunk == 1) {
         if (vec) {
-            reduce_cols_kernel<T, T, OP, true><<<grid, kBlock, 0, st>>>(x, out, outer, r, inner,
-                                                                       chunk, 1, true, r);
+            reduce_cols_kernel<T, T, OP, true, false>
+                <<<grid, kBlock, 0, st>>>(x, out, nullptr, outer, r, inner, chunk, 1, true, r);
         } else {
-            reduce_cols_kernel<T, T, OP, false><<<grid, kBlock, 0, st>>>(x, out, outer, r, inner,
-                                                                        chunk, 1, true, r);
+            reduce_cols_kernel<T, T, OP, false, false>
+                <<<grid, kBlock, 0, st>>>(x, out, nullptr, outer, r, inner, chunk, 1, true, r);
         }
         TP_AMD_HIP_CHECK(hipGetLastError());
         return;
     }
+    // Rows are split only when bx * outer < 2 * cus, so one arrival counter
+    // per column range always fits.
+    TP_AMD_CHECK(outer * bx <= kMaxColCounters, "column reduction: ", outer * bx,
+                 " column ranges exceed the arrival counters");
     Workspace ws(static_cast<size_t>(outer) * nchunk * inner * sizeof(float), device);
     float* partial = static_cast<float*>(ws.get());
+    // One launch: the last block of each column range folds the partials.
     if (vec) {
-        reduce_cols_kernel<T, float, OP, true><<<grid, kBlock, 0, st>>>(
-            x, partial, outer, r, inner, chunk, nchunk, false, r);
+        reduce_cols_kernel<T, float, OP, true, true>
+            <<<grid, kBlock, 0, st>>>(x, partial, out, outer, r, inner, chunk, nchunk, false, r);
     } else {
-        reduce_cols_kernel<T, float, OP, false><<<grid, kBlock, 0, st>>>(
-            x, partial, outer, r, inner, chunk, nchunk, false, r);
-    }
-    TP_AMD_HIP_CHECK(hipGetLastError());
-    // The partials are small; spreading their columns over more blocks (one
-    // float per lane) beats 16-byte packets on a few blocks.
-    const bool vec2 = inner % 4 == 0 && inner / (kColLanes * 4) >= cus;
-    const int64_t cpb2 = static_cast<int64_t>(kColLanes) * (vec2 ? 4 : 1);
-    const dim3 grid2(static_cast<unsigned>((inner + cpb2 - 1) / cpb2), 1u,
-                     static_cast<unsigned>(z));
-    if (vec2) {
-        reduce_cols_kernel<float, T, OP, true><<<grid2, kBlock, 0, st>>>(
-            partial, out, outer, nchunk, inner, nchunk, 1, true, r);
-    } else {
-        reduce_cols_kernel<float, T, OP, false><<<grid2, kBlock, 0, st>>>(
-            partial, out, outer, nchunk, inner, nchunk, 1, true, r);
+        reduce_cols_kernel<T, float, OP, false, true>
+            <<<grid, kBlock, 0, st>>>(x, partial, out, outer, r, inner, chunk, nchunk, false, r);
     }
     TP_AMD_HIP_CHECK(hipGetLastError());
 }

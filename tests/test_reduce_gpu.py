@@ -68,6 +68,30 @@ def test_reductions(dev, ops, orc, dtype):
                             f"amax/amin {dims}")
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(5, 2048, 384), (2, 8192, 3), (3, 700, 1000)],
+                         ids=["outer5-packets", "outer2-scalar", "outer3-ragged"])
+def test_column_reduction_row_chunks(dev, ops, orc, dtype, shape):
+    """Reductions over a middle axis long enough to be split into row chunks,
+    whose partials the last block of each column range folds: several outer
+    indices, a width that takes 16-byte packets, one that does not, and rows
+    that do not divide evenly.  Each reduction runs twice, so an arrival
+    counter left non-zero by the first launch would corrupt the second."""
+    a = sample(orc, shape, dtype, 3)
+    a[0, 5, 1] = orc.from_float(np.array([np.nan], np.float32), dtype)[0]
+    d = dev.from_numpy(a, dtype=dtype)
+    for op, fn in ((SUM, ops.sum_dim), (MEAN, ops.mean_dim), (AMAX, ops.amax), (AMIN, ops.amin)):
+        want = oracle_reduce(orc, op, dtype, a, [1])
+        for rep in range(2):
+            got = fn(d, [1]).numpy()
+            if op in (AMAX, AMIN):
+                assert_bitexact(got, want, f"op {op} run {rep}")
+            else:
+                assert np.array_equal(np.isnan(orc.to_float(got, dtype)), np.isnan(orc.to_float(want, dtype)))
+                ok = ~np.isnan(orc.to_float(want, dtype))
+                assert_normwise(got[ok], want[ok], dtype, 20, f"op {op} run {rep}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_long_reductions(dev, ops, orc, dtype):
     for shape in ((2, 4096), (2, 65536), (16, 8192), (3, 32768), (4096, 2)):
