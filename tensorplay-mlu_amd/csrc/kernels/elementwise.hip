@@ -21,7 +21,10 @@ namespace tp_amd {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+// Packets per thread of the dense kernels.  One 16-byte packet per thread
+// over a grid that covers the tensor streamed at 82 % of HBM on MI355X in a
+// copy of 2 x 256 MB, against 77 % with four packets per thread.
+constexpr int kUnroll = 1;
 
 // 16-bit storage takes the fast transcendental forms (math_ops.h).
 template <typename T>
