@@ -502,7 +502,11 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
         if (vec) chunk = (chunk + N - 1) / N * N;
         nseg = (r + chunk - 1) / chunk;
         const int64_t nsegs = outer * nseg;
-        const bool long_rows = chunk >= 4096;
+        // Four waves share a segment of 4096 elements or more; amax / amin of
+        // 16-bit storage (integer keys) run best one wave a segment up to
+        // 16 KB (measured on 4096-element bf16 rows: 40 us against 45-49 us).
+        const bool key16 = kMinMax<OP> && sizeof(S) == 2;
+        const bool long_rows = key16 ? chunk * 2 >= 16384 : chunk >= 4096;
         auto launch_rows = [&](auto waves_tag, auto vec_tag, auto* dst, bool final_pass) {
             constexpr int W = decltype(waves_tag)::value;
             constexpr bool V = decltype(vec_tag)::value;
