@@ -162,6 +162,84 @@ int tp_amd_launch_strided_copy(int device, int elem_size, int ndim, const int64_
                                void* dst, const int64_t* dst_strides, const void* src,
                                const int64_t* src_strides);
 
+/* ---- neural-network layers (NNKernels.cpp:57-395) ------------------------ */
+
+/* Replaces cnnlLayerNormForward (NNKernels.cpp:88-94): x dense [rows, dim] of
+ * ``dtype``; per row mean = sum(x) / dim, var = sum((x - mean)^2) / dim (the
+ * biased variance), rstd = 1 / sqrt(var + eps), and
+ * y = (x - mean) * rstd * weight + bias.  ``weight`` / ``bias`` ([dim] of
+ * ``dtype``) may be NULL for 1 / 0.  mean and rstd ([rows]) are float32 for
+ * every dtype (stats_dtype, :52-54); float32 arithmetic. */
+int tp_amd_launch_layer_norm(int device, int dtype, int64_t rows, int64_t dim, const void* x,
+                             const void* weight, const void* bias, double eps, void* y,
+                             float* mean, float* rstd);
+
+/* Replaces cnnlLayerNormBackward_v2 (NNKernels.cpp:139-143): from the
+ * forward's input x, its float32 mean and rstd, and grad_out, with
+ * xhat = (x - mean) * rstd and g = grad_out * weight,
+ *   dx      = rstd * (g - mean_row(g) - xhat * mean_row(g * xhat)),
+ *   dweight = sum over rows of grad_out * xhat,
+ *   dbias   = sum over rows of grad_out.
+ * Any of dx, dweight, dbias may be NULL (not computed); ``weight`` may be
+ * NULL for 1.  rows == 0 gives zero parameter gradients. */
+int tp_amd_launch_layer_norm_backward(int device, int dtype, int64_t rows, int64_t dim,
+                                      const void* grad_out, const void* x, const float* mean,
+                                      const float* rstd, const void* weight, void* dx,
+                                      void* dweight, void* dbias);
+
+/* Replaces cnnlFusedDropout_v3 (NNKernels.cpp:184-186): element e of the
+ * dense ``x`` is kept when the uniform (w >> 8) * 2^-24 is >= p, w being word
+ * e % 4 of Philox4x32-10 (Salmon et al., SC 2011) on the counter
+ * (e / 4 low, e / 4 high, offset low, offset high) under the key (seed low,
+ * seed high).  out = keep ? x / (1 - p) : 0 (the scale rounded to float32),
+ * mask = keep (one byte, 0 or 1).  0 <= p < 1. */
+int tp_amd_launch_dropout(int device, int dtype, int64_t n, const void* x, double p,
+                          uint64_t seed, uint64_t offset, void* out, uint8_t* mask);
+
+/* Replaces scaled_product's cnnlOpTensor (NNKernels.cpp:196-220): out = grad *
+ * mask * scale over n dense elements, mask bytes 0 / 1. */
+int tp_amd_launch_dropout_backward(int device, int dtype, int64_t n, const void* grad,
+                                   const uint8_t* mask, double scale, void* out);
+
+/* Replaces cnnlEmbeddingForward_v2 (NNKernels.cpp:254-256): out[i, :] =
+ * weight[indices[i], :] for the n indices (``index_dtype`` int32 or int64);
+ * weight dense [num_weights, dim].  An index outside [0, num_weights) writes
+ * a row of NaN and reads nothing. */
+int tp_amd_launch_embedding(int device, int dtype, int64_t num_weights, int64_t dim,
+                            const void* weight, int index_dtype, int64_t n, const void* indices,
+                            void* out);
+
+/* Replaces cnnlEmbeddingBackward (NNKernels.cpp:283-286): out dense
+ * [num_weights, dim] = sum over i with indices[i] == r of grad[i, :]
+ * (divided by the number of such i when scale_grad_by_freq).  Indices equal
+ * to padding_idx, or outside [0, num_weights), add nothing, so the
+ * padding row is zero.  Accumulated in float32 with atomics (the order of
+ * the additions is not fixed). */
+int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t dim,
+                                     const void* grad, int index_dtype, const void* indices,
+                                     int64_t num_weights, int64_t padding_idx,
+                                     int scale_grad_by_freq, void* out);
+
+/* Replaces cnnlNlllossForward (NNKernels.cpp:350-353): x dense [n, classes],
+ * per sample loss_i = -weight[t_i] * x[i, t_i] and weight w_i = weight[t_i]
+ * (weight NULL: 1); a target equal to ignore_index gives 0 and 0, one
+ * outside [0, classes) NaN and NaN.  reduction 0 writes y[i] = loss_i (and
+ * leaves total_weight alone); 1 (mean) writes y = sum loss / sum w; 2 (sum)
+ * y = sum loss; both write total_weight = sum w.  Sums in a fixed order. */
+int tp_amd_launch_nll_loss(int device, int dtype, int64_t n, int64_t classes, const void* x,
+                           int index_dtype, const void* target, const void* weight,
+                           int reduction, int64_t ignore_index, void* y, void* total_weight);
+
+/* Replaces cnnlNlllossBackward (NNKernels.cpp:385-388): dx dense [n, classes]
+ * is zero except dx[i, t_i] = -weight[t_i] * g_i, with g_i = grad[i]
+ * (reduction 0), grad[0] / total_weight[0] (1) or grad[0] (2); rows whose
+ * target is ignore_index stay zero, rows whose target is outside
+ * [0, classes) are NaN. */
+int tp_amd_launch_nll_loss_backward(int device, int dtype, int64_t n, int64_t classes,
+                                    const void* grad, int index_dtype, const void* target,
+                                    const void* weight, int reduction, int64_t ignore_index,
+                                    const void* total_weight, void* dx);
+
 #ifdef __cplusplus
 }
 #endif

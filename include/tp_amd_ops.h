@@ -167,6 +167,58 @@ int tp_amd__log_softmax_backward_data(const tp_amd_tensor* grad_output,
                                       const tp_amd_tensor* output, int64_t dim,
                                       int input_dtype, tp_amd_tensor* result);
 
+/* ---- neural-network layers (NNKernels.cpp:57-395) ---------------------- */
+/* An output the caller masks off comes back with data == NULL and dtype
+ * TP_AMD_UNDEFINED.  Each entry declines where the reference falls back to
+ * the host. */
+
+/* native_layer_norm (:57-104): normalizes over the trailing dims
+ * ``normalized_shape`` (nnorm entries); weight / bias may be NULL.  Results
+ * y (input's shape and dtype) and float32 mean / rstd of shape [outer].
+ * Declined unless the input is a native float on the device, at least one
+ * leading dim remains, and weight / bias match its device and dtype. */
+int tp_amd_native_layer_norm(const tp_amd_tensor* input, const int64_t* normalized_shape, int nnorm,
+                             const tp_amd_tensor* weight, const tp_amd_tensor* bias, double eps,
+                             tp_amd_tensor* y, tp_amd_tensor* mean, tp_amd_tensor* rstd);
+/* native_layer_norm_backward (:106-159): output_mask (3 ints; NULL = all)
+ * selects dx, dweight, dbias. */
+int tp_amd_native_layer_norm_backward(const tp_amd_tensor* grad_out, const tp_amd_tensor* input,
+                                      const int64_t* normalized_shape, int nnorm,
+                                      const tp_amd_tensor* mean, const tp_amd_tensor* rstd,
+                                      const tp_amd_tensor* weight, const tp_amd_tensor* bias,
+                                      const int* output_mask, tp_amd_tensor* dx,
+                                      tp_amd_tensor* dweight, tp_amd_tensor* dbias);
+/* native_dropout (:163-191): train -1 (unset, i.e. training), 0 or 1; the
+ * random stream is keyed by ``seed`` (the reference draws it from the host
+ * generator, :181-183).  Results out (input's dtype) and a bool mask.  Not
+ * training: a copy and an all-true mask; p == 1: zeros and an all-false
+ * mask. */
+int tp_amd_native_dropout(const tp_amd_tensor* input, double p, int train, uint64_t seed,
+                          tp_amd_tensor* out, tp_amd_tensor* mask);
+/* native_dropout_backward (:222-234): grad_output * mask * scale; the mask
+ * bool or uint8. */
+int tp_amd_native_dropout_backward(const tp_amd_tensor* grad_output, const tp_amd_tensor* mask,
+                                   double scale, tp_amd_tensor* result);
+/* embedding (:242-263): weight [V, D], int32 / int64 indices of any shape;
+ * result [indices..., D].  sparse is declined. */
+int tp_amd_embedding(const tp_amd_tensor* weight, const tp_amd_tensor* indices, int64_t padding_idx,
+                     int scale_grad_by_freq, int sparse, tp_amd_tensor* result);
+/* embedding_dense_backward (:265-296): result [num_weights, D]. */
+int tp_amd_embedding_dense_backward(const tp_amd_tensor* grad_output, const tp_amd_tensor* indices,
+                                    int64_t num_weights, int64_t padding_idx, int scale_grad_by_freq,
+                                    tp_amd_tensor* result);
+/* nll_loss (:327-364): self [N, C], target [N] int32 / int64, weight [C] or
+ * NULL, reduction 0 none / 1 mean / 2 sum.  Results output ([N] or 0-d) and
+ * a 0-d total_weight (0 for reduction none). */
+int tp_amd_nll_loss(const tp_amd_tensor* self, const tp_amd_tensor* target, const tp_amd_tensor* weight,
+                    int64_t reduction, int64_t ignore_index, tp_amd_tensor* output,
+                    tp_amd_tensor* total_weight);
+/* nll_loss_backward (:366-395): result [N, C]. */
+int tp_amd_nll_loss_backward(const tp_amd_tensor* grad_output, const tp_amd_tensor* self,
+                             const tp_amd_tensor* target, const tp_amd_tensor* weight, int64_t reduction,
+                             int64_t ignore_index, const tp_amd_tensor* total_weight,
+                             tp_amd_tensor* result);
+
 /* ---- host-only helpers (Cnnl.cpp:107-205); no device work --------------- */
 
 /* binary_result_dtype (Cnnl.cpp:178-192) for two tensors' dtypes and

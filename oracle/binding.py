@@ -41,6 +41,16 @@ def lib() -> C.CDLL:
         L.orc_gemm_entries.argtypes = [i32, i64, f32, VP, i64, i64, i32, VP, i64, i64, i32, f32,
                                        VP, i64, i64, i64, I64P, i64, VP]
         L.orc_cast.argtypes = [i32, i32, i64, VP, VP]
+        f64, u64 = C.c_double, C.c_uint64
+        L.orc_layer_norm.argtypes = [i32, i64, i64, VP, VP, VP, f64, VP, VP, VP]
+        L.orc_layer_norm_backward.argtypes = [i32, i64, i64, VP, VP, VP, VP, VP, VP, VP, VP]
+        L.orc_philox4x32_10.argtypes = [VP, VP, VP]
+        L.orc_dropout.argtypes = [i32, i64, VP, f64, u64, u64, VP, VP]
+        L.orc_dropout_backward.argtypes = [i32, i64, VP, VP, f64, VP]
+        L.orc_embedding.argtypes = [i32, i64, i64, VP, i32, i64, VP, VP]
+        L.orc_embedding_backward.argtypes = [i32, i64, i64, VP, i32, VP, i64, i64, i32, VP]
+        L.orc_nll_loss.argtypes = [i32, i64, i64, VP, i32, VP, VP, i32, i64, VP, VP]
+        L.orc_nll_loss_backward.argtypes = [i32, i64, i64, VP, i32, VP, VP, i32, i64, VP, VP]
         L.orc_f32_to_bf16.argtypes = [f32]
         L.orc_f32_to_bf16.restype = C.c_uint16
         L.orc_bf16_to_f32.argtypes = [C.c_uint16]
@@ -213,3 +223,120 @@ def cast(src_dtype: int, dst_dtype: int, x: np.ndarray) -> np.ndarray:
     out = np.empty(x.shape, NP[dst_dtype])
     lib().orc_cast(src_dtype, dst_dtype, x.size, _p(x), _p(out))
     return out
+
+
+# ---- neural-network layers ----------------------------------------------------
+
+def _opt(a):
+    return None if a is None else _p(a)
+
+
+def _stats_np(dtype: int):
+    return np.float64 if dtype == F64 else np.float32
+
+
+def _index_code(idx: np.ndarray) -> int:
+    if idx.dtype == np.int32:
+        return I32
+    assert idx.dtype == np.int64, idx.dtype
+    return I64
+
+
+def layer_norm(dtype: int, x, D: int, w=None, b=None, eps: float = 1e-5):
+    """(y, mean, rstd) over the trailing D elements of each row of x."""
+    x = np.ascontiguousarray(x)
+    rows = x.size // D
+    w = None if w is None else np.ascontiguousarray(w)
+    b = None if b is None else np.ascontiguousarray(b)
+    y = np.empty_like(x)
+    mean = np.empty(rows, _stats_np(dtype))
+    rstd = np.empty(rows, _stats_np(dtype))
+    lib().orc_layer_norm(dtype, rows, D, _p(x), _opt(w), _opt(b), eps, _p(y), _p(mean), _p(rstd))
+    return y, mean, rstd
+
+
+def layer_norm_backward(dtype: int, dy, x, D: int, mean, rstd, w=None,
+                        mask=(True, True, True)):
+    """(dx, dw, db), None where ``mask`` says not wanted."""
+    dy, x = np.ascontiguousarray(dy), np.ascontiguousarray(x)
+    rows = x.size // D
+    mean = np.ascontiguousarray(mean, _stats_np(dtype))
+    rstd = np.ascontiguousarray(rstd, _stats_np(dtype))
+    w = None if w is None else np.ascontiguousarray(w)
+    dx = np.empty_like(x) if mask[0] else None
+    dw = np.empty(D, x.dtype) if mask[1] else None
+    db = np.empty(D, x.dtype) if mask[2] else None
+    lib().orc_layer_norm_backward(dtype, rows, D, _p(dy), _p(x), _p(mean), _p(rstd), _opt(w),
+                                  _opt(dx), _opt(dw), _opt(db))
+    return dx, dw, db
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().orc_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def dropout(dtype: int, x, p: float, seed: int, offset: int = 0):
+    """(out, mask) with mask as uint8 0/1."""
+    x = np.ascontiguousarray(x)
+    out = np.empty_like(x)
+    mask = np.empty(x.shape, np.uint8)
+    lib().orc_dropout(dtype, x.size, _p(x), p, seed, offset, _p(out), _p(mask))
+    return out, mask
+
+
+def dropout_backward(dtype: int, grad, mask, scale: float):
+    g = np.ascontiguousarray(grad)
+    m = np.ascontiguousarray(mask, np.uint8)
+    out = np.empty_like(g)
+    lib().orc_dropout_backward(dtype, g.size, _p(g), _p(m), scale, _p(out))
+    return out
+
+
+def embedding(dtype: int, weight, idx):
+    w = np.ascontiguousarray(weight)
+    idx = np.ascontiguousarray(idx)
+    V, D = w.shape
+    out = np.empty(idx.shape + (D,), w.dtype)
+    lib().orc_embedding(dtype, V, D, _p(w), _index_code(idx), idx.size, _p(idx), _p(out))
+    return out
+
+
+def embedding_backward(dtype: int, dy, idx, num_weights: int, padding_idx: int = -1,
+                       scale_grad_by_freq: bool = False):
+    dy = np.ascontiguousarray(dy)
+    idx = np.ascontiguousarray(idx)
+    D = dy.shape[-1]
+    out = np.empty((num_weights, D), dy.dtype)
+    lib().orc_embedding_backward(dtype, idx.size, D, _p(dy), _index_code(idx), _p(idx),
+                                 num_weights, padding_idx, int(scale_grad_by_freq), _p(out))
+    return out
+
+
+def nll_loss(dtype: int, x, target, w=None, reduction: int = 1, ignore_index: int = -100):
+    """(output, total_weight); output has shape (N,) for reduction 0, () otherwise."""
+    x = np.ascontiguousarray(x)
+    t = np.ascontiguousarray(target)
+    w = None if w is None else np.ascontiguousarray(w)
+    n, c = x.shape
+    y = np.empty((n,) if reduction == 0 else (), x.dtype)
+    total = np.empty((), x.dtype)
+    lib().orc_nll_loss(dtype, n, c, _p(x), _index_code(t), _p(t), _opt(w), reduction,
+                       ignore_index, _p(y), _p(total))
+    return y, total
+
+
+def nll_loss_backward(dtype: int, grad, x_shape, target, total, w=None, reduction: int = 1,
+                      ignore_index: int = -100):
+    g = np.ascontiguousarray(grad)
+    t = np.ascontiguousarray(target)
+    tot = np.ascontiguousarray(total)
+    w = None if w is None else np.ascontiguousarray(w)
+    n, c = x_shape
+    dx = np.empty((n, c), g.dtype)
+    lib().orc_nll_loss_backward(dtype, n, c, _p(g), _index_code(t), _p(t), _opt(w), reduction,
+                                ignore_index, _p(tot), _p(dx))
+    return dx

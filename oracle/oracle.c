@@ -7,6 +7,7 @@
 
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -401,6 +402,246 @@ void orc_cast(int sd, int dd, int64_t n, const void* src, void* dst) {
             if (dd == ORC_F64) ((double*)dst)[i] = (double)v;
             else if (is_float_code(dd)) store_float(dd, dst, i, (double)(float)v);
             else store_int(dd, dst, i, v);
+        }
+    }
+}
+
+/* ---- neural-network layers (NNKernels.cpp:57-395) --------------------------------- */
+
+/* Statistics dtype of a layer norm: float32 for the 16-bit floats and
+ * float32, float64 for float64 (stats_dtype, NNKernels.cpp:52-54). */
+static int stats_dtype(int dtype) { return dtype == ORC_F64 ? ORC_F64 : ORC_F32; }
+
+/* Layer norm over rows of D (NNKernels.cpp:59-100): per row the mean and the
+ * biased variance, rstd = 1 / sqrt(var + eps), y = (x - mean) rstd w + b
+ * (w = 1 and b = 0 when absent, :84-87).  mean and rstd are stored in the
+ * statistics dtype. */
+void orc_layer_norm(int dtype, int64_t rows, int64_t D, const void* x, const void* w,
+                    const void* b, double eps, void* y, void* mean, void* rstd) {
+    const int sd = stats_dtype(dtype);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t o = r * D;
+        double s = 0.0;
+        for (int64_t j = 0; j < D; ++j) s += load(dtype, x, o + j);
+        const double mu = s / (double)D;
+        double ss = 0.0;
+        for (int64_t j = 0; j < D; ++j) {
+            const double d = load(dtype, x, o + j) - mu;
+            ss += d * d;
+        }
+        const double rs = 1.0 / sqrt(ss / (double)D + eps);
+        for (int64_t j = 0; j < D; ++j) {
+            const double wj = w ? load(dtype, w, j) : 1.0, bj = b ? load(dtype, b, j) : 0.0;
+            store_float(dtype, y, o + j, (load(dtype, x, o + j) - mu) * rs * wj + bj);
+        }
+        store_float(sd, mean, r, mu);
+        store_float(sd, rstd, r, rs);
+    }
+}
+
+/* Layer norm backward (NNKernels.cpp:104-160) from the saved statistics:
+ * xhat = (x - mean) rstd, g = dy w,
+ * dx = rstd (g - mean_j(g) - xhat mean_j(g xhat)),
+ * dw = sum over rows of dy xhat, db = sum over rows of dy.
+ * Any of dx, dw, db may be NULL (not asked for). */
+void orc_layer_norm_backward(int dtype, int64_t rows, int64_t D, const void* dy, const void* x,
+                             const void* mean, const void* rstd, const void* w, void* dx,
+                             void* dw, void* db) {
+    const int sd = stats_dtype(dtype);
+    if (dx) {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const int64_t o = r * D;
+            const double mu = load(sd, mean, r), rs = load(sd, rstd, r);
+            double sg = 0.0, sgx = 0.0;
+            for (int64_t j = 0; j < D; ++j) {
+                const double g = load(dtype, dy, o + j) * (w ? load(dtype, w, j) : 1.0);
+                sg += g;
+                sgx += g * (load(dtype, x, o + j) - mu) * rs;
+            }
+            const double mg = sg / (double)D, mgx = sgx / (double)D;
+            for (int64_t j = 0; j < D; ++j) {
+                const double g = load(dtype, dy, o + j) * (w ? load(dtype, w, j) : 1.0);
+                const double xh = (load(dtype, x, o + j) - mu) * rs;
+                store_float(dtype, dx, o + j, rs * (g - mg - xh * mgx));
+            }
+        }
+    }
+    if (dw || db) {
+#pragma omp parallel for schedule(static)
+        for (int64_t j = 0; j < D; ++j) {
+            double aw = 0.0, ab = 0.0;
+            for (int64_t r = 0; r < rows; ++r) {
+                const double g = load(dtype, dy, r * D + j);
+                aw += g * (load(dtype, x, r * D + j) - load(sd, mean, r)) * load(sd, rstd, r);
+                ab += g;
+            }
+            if (dw) store_float(dtype, dw, j, aw);
+            if (db) store_float(dtype, db, j, ab);
+        }
+    }
+}
+
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+ * easy as 1, 2, 3", SC 2011): ten rounds; a round multiplies counter words 0
+ * and 2 by the round constants into 64-bit products and recombines the
+ * halves with words 1 and 3 and the key, which is bumped by the Weyl
+ * constants between rounds. */
+void orc_philox4x32_10(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round) {
+        if (round > 0) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+        c0 = n0;
+        c1 = n1;
+        c2 = n2;
+        c3 = n3;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+/* Dropout on the Philox stream (NNKernels.cpp:164-205): element e takes word
+ * e % 4 of the block for counter (e / 4 as 64 bits, offset as 64 bits) under
+ * key seed; its uniform (word >> 8) 2^-24 keeps it when >= p; out = x / (1 - p)
+ * where kept, else 0; mask is 1 where kept. */
+void orc_dropout(int dtype, int64_t n, const void* x, double p, uint64_t seed, uint64_t offset,
+                 void* out, uint8_t* mask) {
+    const double scale = 1.0 / (1.0 - p);
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+#pragma omp parallel for schedule(static)
+    for (int64_t blk = 0; blk < (n + 3) / 4; ++blk) {
+        const uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)((uint64_t)blk >> 32), (uint32_t)offset,
+                                 (uint32_t)(offset >> 32)};
+        uint32_t word[4];
+        orc_philox4x32_10(ctr, key, word);
+        for (int j = 0; j < 4 && blk * 4 + j < n; ++j) {
+            const int64_t e = blk * 4 + j;
+            const int keep = ldexp((double)(word[j] >> 8), -24) >= p;
+            mask[e] = (uint8_t)keep;
+            store_float(dtype, out, e, keep ? load(dtype, x, e) * scale : 0.0);
+        }
+    }
+}
+
+/* out = grad * mask * scale (NNKernels.cpp:196-236). */
+void orc_dropout_backward(int dtype, int64_t n, const void* grad, const uint8_t* mask,
+                          double scale, void* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < n; ++e) {
+        store_float(dtype, out, e, load(dtype, grad, e) * (mask[e] ? 1.0 : 0.0) * scale);
+    }
+}
+
+static int64_t index_at(int index_dtype, const void* idx, int64_t i) {
+    return index_dtype == ORC_I32 ? ((const int32_t*)idx)[i] : ((const int64_t*)idx)[i];
+}
+
+/* Embedding lookup (NNKernels.cpp:242-270): out[i, :] = weight[idx[i], :].
+ * An index outside [0, V) gives a NaN row (the host kernel raises instead;
+ * what the device returns for it is parity unpinned). */
+void orc_embedding(int dtype, int64_t V, int64_t D, const void* weight, int index_dtype,
+                   int64_t n, const void* idx, void* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t r = index_at(index_dtype, idx, i);
+        for (int64_t j = 0; j < D; ++j) {
+            store_float(dtype, out, i * D + j, r >= 0 && r < V ? load(dtype, weight, r * D + j) : NAN);
+        }
+    }
+}
+
+/* Dense embedding gradient (NNKernels.cpp:272-300): row r of the result is
+ * the sum of dy[i, :] over the samples with idx[i] == r, each divided by the
+ * number of such samples with scale_grad_by_freq; the padding row and rows
+ * never indexed are zero; indices outside [0, V) add nothing. */
+void orc_embedding_backward(int dtype, int64_t n, int64_t D, const void* dy, int index_dtype,
+                            const void* idx, int64_t V, int64_t padding_idx,
+                            int scale_grad_by_freq, void* out) {
+#pragma omp parallel
+    {
+        double* acc = (double*)malloc((size_t)(D > 0 ? D : 1) * sizeof(double));
+#pragma omp for schedule(dynamic, 16)
+        for (int64_t r = 0; r < V; ++r) {
+            int64_t count = 0;
+            for (int64_t j = 0; j < D; ++j) acc[j] = 0.0;
+            if (r != padding_idx) {
+                for (int64_t i = 0; i < n; ++i) {
+                    if (index_at(index_dtype, idx, i) != r) continue;
+                    ++count;
+                    for (int64_t j = 0; j < D; ++j) acc[j] += load(dtype, dy, i * D + j);
+                }
+            }
+            const double scale = scale_grad_by_freq && count > 0 ? 1.0 / (double)count : 1.0;
+            for (int64_t j = 0; j < D; ++j) store_float(dtype, out, r * D + j, acc[j] * scale);
+        }
+        free(acc);
+    }
+}
+
+/* Per-sample NLL term: -w[t] x[i, t] with weight w[t]; 0 and 0 for
+ * ignore_index; NaN and NaN for a target outside [0, C) (the host kernel
+ * raises; parity unpinned). */
+static void nll_term(int dtype, int64_t C, const void* x, int64_t i, int64_t t, const void* w,
+                     int64_t ignore_index, double* loss, double* wt) {
+    *loss = 0.0;
+    *wt = 0.0;
+    if (t == ignore_index) return;
+    if (t < 0 || t >= C) {
+        *loss = *wt = NAN;
+        return;
+    }
+    *wt = w ? load(dtype, w, t) : 1.0;
+    *loss = -*wt * load(dtype, x, i * C + t);
+}
+
+/* nll_loss over (N, C) with (N) targets (NNKernels.cpp:327-363): reduction 0
+ * gives the per-sample terms and a zero total; 1 (mean) the sum of terms over
+ * the sum of weights; 2 (sum) the sum; total is the sum of weights. */
+void orc_nll_loss(int dtype, int64_t n, int64_t C, const void* x, int index_dtype,
+                  const void* target, const void* w, int reduction, int64_t ignore_index,
+                  void* y, void* total) {
+    double sl = 0.0, sw = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        double l, wt;
+        nll_term(dtype, C, x, i, index_at(index_dtype, target, i), w, ignore_index, &l, &wt);
+        if (reduction == 0) store_float(dtype, y, i, l);
+        sl += l;
+        sw += wt;
+    }
+    if (reduction == 0) {
+        store_float(dtype, total, 0, 0.0);
+        return;
+    }
+    store_float(dtype, y, 0, reduction == 1 ? sl / sw : sl);
+    store_float(dtype, total, 0, sw);
+}
+
+/* nll_loss backward (NNKernels.cpp:365-395): dx[i, t_i] = -w[t_i] g_i with
+ * g_i = grad[i] (none), grad[0] / total (mean) or grad[0] (sum); other entries
+ * 0; a NaN row for a target outside [0, C) that is not ignore_index. */
+void orc_nll_loss_backward(int dtype, int64_t n, int64_t C, const void* grad, int index_dtype,
+                           const void* target, const void* w, int reduction, int64_t ignore_index,
+                           const void* total, void* dx) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t t = index_at(index_dtype, target, i);
+        const int bad = t != ignore_index && (t < 0 || t >= C);
+        double g = reduction == 0 ? load(dtype, grad, i) : load(dtype, grad, 0);
+        if (reduction == 1) g /= load(dtype, total, 0);
+        for (int64_t c = 0; c < C; ++c) {
+            double v = 0.0;
+            if (bad) v = NAN;
+            else if (t != ignore_index && c == t) v = -(w ? load(dtype, w, t) : 1.0) * g;
+            store_float(dtype, dx, i * C + c, v);
         }
     }
 }

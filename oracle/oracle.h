@@ -31,9 +31,26 @@
  *   orc_cast, rounding helpers   numpy astype (float16, integers); bfloat16 by
  *                                brute force over all 2^16 patterns and the
  *                                nearest-neighbour/ties-to-even property
+ *   orc_layer_norm(_backward)    torch float64 layer_norm and its autograd
+ *                                gradients; central finite differences of the
+ *                                float64 forward; shift/scale invariance and
+ *                                the constant row (tests/test_oracle_nn.py)
+ *   orc_philox4x32_10            the Random123 known-answer vectors
+ *   orc_dropout(_backward)       the first Philox block's words by hand, the
+ *                                keep fraction, out = x mask / (1 - p)
+ *   orc_embedding(_backward)     numpy fancy indexing; torch float64 autograd
+ *                                with padding_idx and scale_grad_by_freq; the
+ *                                one-hot product onehot(idx)^T dy
+ *   orc_nll_loss(_backward)      torch float64 nll_loss (weights, ignore_index,
+ *                                the three reductions) and its autograd
+ *                                gradient; -sum x[i, t_i] by hand
  * NaN semantics of amax/amin/relu against TensorPlay's host kernels, and
  * integer conversions outside the target range, are "parity unpinned": no
- * reference test or fixture fixes them.
+ * reference test or fixture fixes them.  So are the NN layers' results for
+ * an index or target outside its table (the host kernels raise, the device
+ * returns NaN), and dropout's exact random stream: CNNL's Philox stream is
+ * closed, so the oracle fixes the published Philox4x32-10 and the tests
+ * check the mask's distribution and out = x mask / (1 - p).
  */
 #ifndef TP_AMD_ORACLE_H
 #define TP_AMD_ORACLE_H
@@ -75,5 +92,27 @@ void orc_gemm_entries(int dtype, int64_t k, float alpha, const void* a, int64_t 
                       int trans_b, float beta, const void* cin, int64_t cin_rs, int64_t cin_cs,
                       int64_t cin_stride_b, const int64_t* bij, int64_t count, double* out);
 void orc_cast(int src_dtype, int dst_dtype, int64_t n, const void* src, void* dst);
+
+void orc_layer_norm(int dtype, int64_t rows, int64_t D, const void* x, const void* w,
+                    const void* b, double eps, void* y, void* mean, void* rstd);
+void orc_layer_norm_backward(int dtype, int64_t rows, int64_t D, const void* dy, const void* x,
+                             const void* mean, const void* rstd, const void* w, void* dx,
+                             void* dw, void* db);
+void orc_philox4x32_10(const uint32_t* ctr, const uint32_t* key, uint32_t* out);
+void orc_dropout(int dtype, int64_t n, const void* x, double p, uint64_t seed, uint64_t offset,
+                 void* out, uint8_t* mask);
+void orc_dropout_backward(int dtype, int64_t n, const void* grad, const uint8_t* mask,
+                          double scale, void* out);
+void orc_embedding(int dtype, int64_t V, int64_t D, const void* weight, int index_dtype,
+                   int64_t n, const void* idx, void* out);
+void orc_embedding_backward(int dtype, int64_t n, int64_t D, const void* dy, int index_dtype,
+                            const void* idx, int64_t V, int64_t padding_idx,
+                            int scale_grad_by_freq, void* out);
+void orc_nll_loss(int dtype, int64_t n, int64_t C, const void* x, int index_dtype,
+                  const void* target, const void* w, int reduction, int64_t ignore_index,
+                  void* y, void* total);
+void orc_nll_loss_backward(int dtype, int64_t n, int64_t C, const void* grad, int index_dtype,
+                           const void* target, const void* w, int reduction, int64_t ignore_index,
+                           const void* total, void* dx);
 
 #endif

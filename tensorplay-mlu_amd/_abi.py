@@ -59,6 +59,7 @@ T = C.POINTER(Tensor)
 I64P = C.POINTER(C.c_int64)
 VP = C.c_void_p
 i32, i64, f32, f64 = C.c_int, C.c_int64, C.c_float, C.c_double
+u64 = C.c_uint64
 
 # name -> (restype, argtypes)
 PROTOTYPES = {
@@ -102,6 +103,17 @@ PROTOTYPES = {
     "tp_amd_launch_cast": (i32, [i32, i32, i32, i64, VP, VP]),
     "tp_amd_launch_fill": (i32, [i32, i32, VP, i32, I64P, VP, I64P]),
     "tp_amd_launch_strided_copy": (i32, [i32, i32, i32, I64P, VP, I64P, VP, I64P]),
+    "tp_amd_launch_layer_norm": (i32, [i32, i32, i64, i64, VP, VP, VP, f64, VP, VP, VP]),
+    "tp_amd_launch_layer_norm_backward": (i32, [i32, i32, i64, i64, VP, VP, VP, VP, VP, VP, VP,
+                                                VP]),
+    "tp_amd_launch_dropout": (i32, [i32, i32, i64, VP, f64, u64, u64, VP, VP]),
+    "tp_amd_launch_dropout_backward": (i32, [i32, i32, i64, VP, VP, f64, VP]),
+    "tp_amd_launch_embedding": (i32, [i32, i32, i64, i64, VP, i32, i64, VP, VP]),
+    "tp_amd_launch_embedding_backward": (i32, [i32, i32, i64, i64, VP, i32, VP, i64, i64, i32,
+                                               VP]),
+    "tp_amd_launch_nll_loss": (i32, [i32, i32, i64, i64, VP, i32, VP, VP, i32, i64, VP, VP]),
+    "tp_amd_launch_nll_loss_backward": (i32, [i32, i32, i64, i64, VP, i32, VP, VP, i32, i64, VP,
+                                              VP]),
     # operators (tp_amd_ops.h)
     "tp_amd_empty": (i32, [I64P, i32, i32, i32, i32, T]),
     "tp_amd_empty_like": (i32, [T, i32, i32, T]),
@@ -166,6 +178,15 @@ PROTOTYPES = {
     "tp_amd__log_softmax": (i32, [T, i64, i32, T]),
     "tp_amd__softmax_backward_data": (i32, [T, T, i64, i32, T]),
     "tp_amd__log_softmax_backward_data": (i32, [T, T, i64, i32, T]),
+    "tp_amd_native_layer_norm": (i32, [T, I64P, i32, T, T, f64, T, T, T]),
+    "tp_amd_native_layer_norm_backward": (i32, [T, T, I64P, i32, T, T, T, T, C.POINTER(C.c_int),
+                                                T, T, T]),
+    "tp_amd_native_dropout": (i32, [T, f64, i32, u64, T, T]),
+    "tp_amd_native_dropout_backward": (i32, [T, T, f64, T]),
+    "tp_amd_embedding": (i32, [T, T, i64, i32, i32, T]),
+    "tp_amd_embedding_dense_backward": (i32, [T, T, i64, i64, i32, T]),
+    "tp_amd_nll_loss": (i32, [T, T, T, i64, i64, T, T]),
+    "tp_amd_nll_loss_backward": (i32, [T, T, T, T, i64, i64, T, T]),
     "tp_amd_binary_result_dtype": (i32, [i32, i32, i32, i32]),
     "tp_amd_broadcast_shape": (i32, [I64P, i32, I64P, i32, I64P, C.POINTER(C.c_int)]),
     "tp_amd_is_dense": (i32, [T]),

@@ -1,17 +1,21 @@
-// The 64 PrivateUse1 operator registrations of the hot path, each a thin
-// wrapper over one operator C-ABI entry (tp_amd_ops.h).  The C-ABI keeps the
+// The 72 PrivateUse1 operator registrations (the 64 of the hot path and the
+// 8 neural-network layers), each a thin wrapper over one operator C-ABI
+// entry (tp_amd_ops.h).  The C-ABI keeps the
 // reference operators' dtype rules and decline conditions; when it declines
 // (TP_AMD_DECLINED), or a tensor cannot be described as a view, the wrapper
 // runs TensorPlay's host kernel through cpu_fallback, as the reference does.
 //
 // Registration blocks mirror tensorplay_mlu/csrc/CopyKernels.cpp:349-364,
 // BinaryKernels.cpp:252-269, UnaryKernels.cpp:291-310,
-// BlasKernels.cpp:416-422 and ReduceKernels.cpp:267-282: same operator
-// names, same signature types.
+// BlasKernels.cpp:416-422, ReduceKernels.cpp:267-282 and
+// NNKernels.cpp:399-410: same operator names, same signature types.
 
+#include <array>
 #include <functional>
+#include <tuple>
 
 #include "Adapter.h"
+#include "Generator.h"
 
 namespace tensorplay {
 namespace amd {
@@ -623,6 +627,172 @@ Tensor log_softmax_backward_kernel(const Tensor& grad_output, const Tensor& outp
                                                                        input_dtype);
 }
 
+// ---- neural-network layers (reference NNKernels.cpp:57-395) ---------------
+
+// An optional tensor as a view pointer: nullptr when absent; false when it
+// cannot be described (the host kernel runs).
+bool optional_view(const std::optional<Tensor>& t, tp_amd_tensor* storage,
+                   const tp_amd_tensor** out) {
+    if (!t.has_value() || !t->defined()) {
+        *out = nullptr;
+        return true;
+    }
+    if (!view(*t, storage)) return false;
+    *out = storage;
+    return true;
+}
+
+// An entry with N result slots.
+template <size_t N, typename F>
+std::optional<std::array<tp_amd_tensor, N>> produce_n(const char* op, F&& call) {
+    std::array<tp_amd_tensor, N> r{};
+    const int status = call(r.data());
+    if (status == TP_AMD_DECLINED) return std::nullopt;
+    if (status != TP_AMD_OK) raise(op);
+    return r;
+}
+
+// A slot the entry left undefined (an output masked off) is an undefined
+// tensor.
+Tensor adopt_optional(const tp_amd_tensor& r) {
+    return r.data == nullptr && r.dtype == TP_AMD_UNDEFINED ? Tensor() : adopt(r);
+}
+
+std::tuple<Tensor, Tensor, Tensor> native_layer_norm_kernel(
+    const Tensor& input, const std::vector<int64_t>& normalized_shape,
+    const std::optional<Tensor>& weight, const std::optional<Tensor>& bias, double eps) {
+    tp_amd_tensor x, ws, bs;
+    const tp_amd_tensor *w = nullptr, *b = nullptr;
+    if (view(input, &x) && optional_view(weight, &ws, &w) && optional_view(bias, &bs, &b)) {
+        auto r = produce_n<3>("native_layer_norm", [&](tp_amd_tensor* out) {
+            return tp_amd_native_layer_norm(&x, normalized_shape.data(),
+                                            static_cast<int>(normalized_shape.size()), w, b, eps,
+                                            &out[0], &out[1], &out[2]);
+        });
+        if (r) return {adopt((*r)[0]), adopt((*r)[1]), adopt((*r)[2])};
+    }
+    return cpu_fallback::Kernel<"native_layer_norm", sig::native_layer_norm>::call(
+        input, normalized_shape, weight, bias, eps);
+}
+
+std::tuple<Tensor, Tensor, Tensor> native_layer_norm_backward_kernel(
+    const Tensor& grad_out, const Tensor& input, const std::vector<int64_t>& normalized_shape,
+    const Tensor& mean, const Tensor& rstd, const std::optional<Tensor>& weight,
+    const std::optional<Tensor>& bias, const std::vector<bool>& output_mask) {
+    tp_amd_tensor g, x, m, r, ws, bs;
+    const tp_amd_tensor *w = nullptr, *b = nullptr;
+    int mask[3] = {1, 1, 1};
+    for (size_t i = 0; i < 3 && i < output_mask.size(); ++i) mask[i] = output_mask[i] ? 1 : 0;
+    if (view(grad_out, &g) && view(input, &x) && view(mean, &m) && view(rstd, &r) &&
+        optional_view(weight, &ws, &w) && optional_view(bias, &bs, &b)) {
+        auto res = produce_n<3>("native_layer_norm_backward", [&](tp_amd_tensor* out) {
+            return tp_amd_native_layer_norm_backward(
+                &g, &x, normalized_shape.data(), static_cast<int>(normalized_shape.size()), &m, &r,
+                w, b, mask, &out[0], &out[1], &out[2]);
+        });
+        if (res) {
+            return {adopt_optional((*res)[0]), adopt_optional((*res)[1]),
+                    adopt_optional((*res)[2])};
+        }
+    }
+    return cpu_fallback::Kernel<"native_layer_norm_backward", sig::native_layer_norm_backward>::
+        call(grad_out, input, normalized_shape, mean, rstd, weight, bias, output_mask);
+}
+
+std::tuple<Tensor, Tensor> native_dropout_kernel(const Tensor& input, double p,
+                                                 std::optional<bool> train) {
+    tp_amd_tensor x;
+    if (view(input, &x)) {
+        const int t = train.has_value() ? (*train ? 1 : 0) : -1;
+        // One 64-bit draw from TensorPlay's host generator keys the Philox
+        // stream, so a manual seed repeats the mask.
+        const uint64_t seed = default_generator().random64();
+        auto r = produce_n<2>("native_dropout", [&](tp_amd_tensor* out) {
+            return tp_amd_native_dropout(&x, p, t, seed, &out[0], &out[1]);
+        });
+        if (r) return {adopt((*r)[0]), adopt((*r)[1])};
+    }
+    return cpu_fallback::Kernel<"native_dropout", sig::native_dropout>::call(input, p, train);
+}
+
+Tensor native_dropout_backward_kernel(const Tensor& grad_output, const Tensor& mask,
+                                      double scale) {
+    tp_amd_tensor g, m;
+    if (view(grad_output, &g) && view(mask, &m)) {
+        if (auto r = produce("native_dropout_backward", [&](tp_amd_tensor* out) {
+                return tp_amd_native_dropout_backward(&g, &m, scale, out);
+            })) {
+            return *r;
+        }
+    }
+    return cpu_fallback::Kernel<"native_dropout_backward", sig::native_dropout_backward>::call(
+        grad_output, mask, scale);
+}
+
+Tensor embedding_kernel(const Tensor& weight, const Tensor& indices, int64_t padding_idx,
+                        bool scale_grad_by_freq, bool sparse) {
+    tp_amd_tensor w, i;
+    if (view(weight, &w) && view(indices, &i)) {
+        if (auto r = produce("embedding", [&](tp_amd_tensor* out) {
+                return tp_amd_embedding(&w, &i, padding_idx, scale_grad_by_freq ? 1 : 0,
+                                        sparse ? 1 : 0, out);
+            })) {
+            return *r;
+        }
+    }
+    return cpu_fallback::Kernel<"embedding", sig::embedding>::call(weight, indices, padding_idx,
+                                                                   scale_grad_by_freq, sparse);
+}
+
+Tensor embedding_dense_backward_kernel(const Tensor& grad_output, const Tensor& indices,
+                                       int64_t num_weights, int64_t padding_idx,
+                                       bool scale_grad_by_freq) {
+    tp_amd_tensor g, i;
+    if (view(grad_output, &g) && view(indices, &i)) {
+        if (auto r = produce("embedding_dense_backward", [&](tp_amd_tensor* out) {
+                return tp_amd_embedding_dense_backward(&g, &i, num_weights, padding_idx,
+                                                       scale_grad_by_freq ? 1 : 0, out);
+            })) {
+            return *r;
+        }
+    }
+    return cpu_fallback::Kernel<"embedding_dense_backward", sig::embedding_dense_backward>::call(
+        grad_output, indices, num_weights, padding_idx, scale_grad_by_freq);
+}
+
+std::tuple<Tensor, Tensor> nll_loss_kernel(const Tensor& self, const Tensor& target,
+                                           const std::optional<Tensor>& weight, int64_t reduction,
+                                           int64_t ignore_index) {
+    tp_amd_tensor x, t, ws;
+    const tp_amd_tensor* w = nullptr;
+    if (view(self, &x) && view(target, &t) && optional_view(weight, &ws, &w)) {
+        auto r = produce_n<2>("nll_loss", [&](tp_amd_tensor* out) {
+            return tp_amd_nll_loss(&x, &t, w, reduction, ignore_index, &out[0], &out[1]);
+        });
+        if (r) return {adopt((*r)[0]), adopt((*r)[1])};
+    }
+    return cpu_fallback::Kernel<"nll_loss", sig::nll_loss>::call(self, target, weight, reduction,
+                                                                 ignore_index);
+}
+
+Tensor nll_loss_backward_kernel(const Tensor& grad_output, const Tensor& self,
+                                const Tensor& target, const std::optional<Tensor>& weight,
+                                int64_t reduction, int64_t ignore_index,
+                                const Tensor& total_weight) {
+    tp_amd_tensor g, x, t, ws, tw;
+    const tp_amd_tensor* w = nullptr;
+    if (view(grad_output, &g) && view(self, &x) && view(target, &t) &&
+        optional_view(weight, &ws, &w) && view(total_weight, &tw)) {
+        if (auto r = produce("nll_loss_backward", [&](tp_amd_tensor* out) {
+                return tp_amd_nll_loss_backward(&g, &x, &t, w, reduction, ignore_index, &tw, out);
+            })) {
+            return *r;
+        }
+    }
+    return cpu_fallback::Kernel<"nll_loss_backward", sig::nll_loss_backward>::call(
+        grad_output, self, target, weight, reduction, ignore_index, total_weight);
+}
+
 }  // namespace
 
 }  // namespace amd
@@ -711,6 +881,20 @@ TENSORPLAY_LIBRARY_IMPL(PrivateUse1, AmdReduceKernels) {
            static_cast<sig::_softmax_backward_data*>(&softmax_backward_kernel));
     m.impl("_log_softmax_backward_data",
            static_cast<sig::_log_softmax_backward_data*>(&log_softmax_backward_kernel));
+}
+
+TENSORPLAY_LIBRARY_IMPL(PrivateUse1, AmdNNKernels) {
+    m.impl("native_layer_norm", static_cast<sig::native_layer_norm*>(&native_layer_norm_kernel));
+    m.impl("native_layer_norm_backward",
+           static_cast<sig::native_layer_norm_backward*>(&native_layer_norm_backward_kernel));
+    m.impl("native_dropout", static_cast<sig::native_dropout*>(&native_dropout_kernel));
+    m.impl("native_dropout_backward",
+           static_cast<sig::native_dropout_backward*>(&native_dropout_backward_kernel));
+    m.impl("embedding", static_cast<sig::embedding*>(&embedding_kernel));
+    m.impl("embedding_dense_backward",
+           static_cast<sig::embedding_dense_backward*>(&embedding_dense_backward_kernel));
+    m.impl("nll_loss", static_cast<sig::nll_loss*>(&nll_loss_kernel));
+    m.impl("nll_loss_backward", static_cast<sig::nll_loss_backward*>(&nll_loss_backward_kernel));
 }
 
 }  // namespace tensorplay

@@ -356,8 +356,74 @@ def _log_softmax_backward_data(grad_output, output, dim, input_dtype):
                         dim, dtype_code(input_dtype))
 
 
-#: The 64 operator names of the reference's registrations and the function
-#: here that serves each.
+# ---- neural-network layers (NNKernels.cpp:57-395) -------------------------------
+
+
+def _call_results(fn, *args, count):
+    """An entry with ``count`` result slots; a slot the call leaves undefined
+    (an output masked off) comes back as None."""
+    outs = [_abi.Tensor() for _ in range(count)]
+    try:
+        check(fn(*args, *[C.byref(o) for o in outs]))
+    finally:
+        _keep.clear()
+    return tuple(None if (not o.data and o.dtype == _abi.UNDEFINED) else DeviceTensor.from_result(o)
+                 for o in outs)
+
+
+def native_layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
+    """(y, mean, rstd); mean and rstd are float32 of shape [outer]."""
+    shape, n = _dims(list(normalized_shape))
+    return _call_results(L().tp_amd_native_layer_norm, _ref(input), shape, n, _ref(weight),
+                         _ref(bias), float(eps), count=3)
+
+
+def native_layer_norm_backward(grad_out, input, normalized_shape, mean, rstd, weight=None,
+                               bias=None, output_mask=(True, True, True)):
+    """(dx, dweight, dbias), None where output_mask is False."""
+    shape, n = _dims(list(normalized_shape))
+    mask = (C.c_int * 3)(*[int(bool(m)) for m in output_mask])
+    return _call_results(L().tp_amd_native_layer_norm_backward, _ref(grad_out), _ref(input), shape,
+                         n, _ref(mean), _ref(rstd), _ref(weight), _ref(bias), mask, count=3)
+
+
+def native_dropout(input, p, train=None, seed=0):
+    """(out, mask); ``train`` None counts as training.  The stream of random
+    numbers is keyed by ``seed``."""
+    t = -1 if train is None else int(bool(train))
+    return _call_results(L().tp_amd_native_dropout, _ref(input), float(p), t,
+                         int(seed) & 0xFFFFFFFFFFFFFFFF, count=2)
+
+
+def native_dropout_backward(grad_output, mask, scale):
+    return _call_result(L().tp_amd_native_dropout_backward, _ref(grad_output), _ref(mask),
+                        float(scale))
+
+
+def embedding(weight, indices, padding_idx=-1, scale_grad_by_freq=False, sparse=False):
+    return _call_result(L().tp_amd_embedding, _ref(weight), _ref(indices), int(padding_idx),
+                        int(bool(scale_grad_by_freq)), int(bool(sparse)))
+
+
+def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1,
+                             scale_grad_by_freq=False):
+    return _call_result(L().tp_amd_embedding_dense_backward, _ref(grad_output), _ref(indices),
+                        int(num_weights), int(padding_idx), int(bool(scale_grad_by_freq)))
+
+
+def nll_loss(self, target, weight=None, reduction=1, ignore_index=-100):
+    """(output, total_weight); reduction 0 none, 1 mean, 2 sum."""
+    return _call_results(L().tp_amd_nll_loss, _ref(self), _ref(target), _ref(weight),
+                         int(reduction), int(ignore_index), count=2)
+
+
+def nll_loss_backward(grad_output, self, target, weight, reduction, ignore_index, total_weight):
+    return _call_result(L().tp_amd_nll_loss_backward, _ref(grad_output), _ref(self), _ref(target),
+                        _ref(weight), int(reduction), int(ignore_index), _ref(total_weight))
+
+
+#: The 72 operator names of the reference's registrations (64 on the hot
+#: path, 8 neural-network layers) and the function here that serves each.
 REGISTRATIONS = {
     "empty_like": empty_like, "zeros_like": zeros_like, "ones_like": ones_like,
     "full_like": full_like, "item": item, "_local_scalar_dense": _local_scalar_dense,
@@ -379,4 +445,9 @@ REGISTRATIONS = {
     "_softmax": _softmax, "_log_softmax": _log_softmax,
     "_softmax_backward_data": _softmax_backward_data,
     "_log_softmax_backward_data": _log_softmax_backward_data,
+    "native_layer_norm": native_layer_norm,
+    "native_layer_norm_backward": native_layer_norm_backward,
+    "native_dropout": native_dropout, "native_dropout_backward": native_dropout_backward,
+    "embedding": embedding, "embedding_dense_backward": embedding_dense_backward,
+    "nll_loss": nll_loss, "nll_loss_backward": nll_loss_backward,
 }

@@ -1,6 +1,7 @@
 // Signature types of the operators the adapter registers, written from the
 // reference kernel definitions (tensorplay_mlu/csrc/*Kernels.cpp).
 #pragma once
+#include <tuple>
 #include <optional>
 #include <string>
 #include <vector>
@@ -80,5 +81,20 @@ using _softmax = Tensor(const Tensor&, int64_t, bool);
 using _log_softmax = _softmax;
 using _softmax_backward_data = Tensor(const Tensor&, const Tensor&, int64_t, DType);
 using _log_softmax_backward_data = _softmax_backward_data;
+
+using native_layer_norm = std::tuple<Tensor, Tensor, Tensor>(const Tensor&, const IntList&,
+                                                             const std::optional<Tensor>&,
+                                                             const std::optional<Tensor>&, double);
+using native_layer_norm_backward = std::tuple<Tensor, Tensor, Tensor>(
+    const Tensor&, const Tensor&, const IntList&, const Tensor&, const Tensor&,
+    const std::optional<Tensor>&, const std::optional<Tensor>&, const std::vector<bool>&);
+using native_dropout = std::tuple<Tensor, Tensor>(const Tensor&, double, std::optional<bool>);
+using native_dropout_backward = Tensor(const Tensor&, const Tensor&, double);
+using embedding = Tensor(const Tensor&, const Tensor&, int64_t, bool, bool);
+using embedding_dense_backward = Tensor(const Tensor&, const Tensor&, int64_t, int64_t, bool);
+using nll_loss = std::tuple<Tensor, Tensor>(const Tensor&, const Tensor&,
+                                            const std::optional<Tensor>&, int64_t, int64_t);
+using nll_loss_backward = Tensor(const Tensor&, const Tensor&, const Tensor&,
+                                 const std::optional<Tensor>&, int64_t, int64_t, const Tensor&);
 }  // namespace kernel_signatures
 }  // namespace tensorplay

@@ -40,9 +40,9 @@ def test_bindings_cover_every_declared_symbol():
     assert declared_functions() == set(abi.PROTOTYPES)
 
 
-def test_ops_mirror_the_64_registrations(amd):
+def test_ops_mirror_the_72_registrations(amd):
     ops = importlib.import_module("tensorplay-mlu_amd.ops")
-    assert len(ops.REGISTRATIONS) == 64
+    assert len(ops.REGISTRATIONS) == 72
     assert all(callable(f) for f in ops.REGISTRATIONS.values())
 
 
@@ -72,13 +72,14 @@ def test_oracle_builds_and_exports():
 ADAPTER = os.path.join(ROOT, "tensorplay-mlu_amd", "csrc", "tensorplay")
 
 
-def test_tensorplay_adapter_registers_the_64_operators():
+def test_tensorplay_adapter_registers_the_72_operators():
     """The adapter's registration blocks name exactly the operators of the
-    reference's five hot-path blocks (the Python mirror lists the same)."""
+    reference's five hot-path blocks and its NN block (the Python mirror
+    lists the same)."""
     ops = importlib.import_module("tensorplay-mlu_amd.ops")
     text = open(os.path.join(ADAPTER, "Kernels.cpp")).read()
     names = re.findall(r'm\.impl\(\s*"([^"]+)"', text)
-    assert len(names) == 64 and len(set(names)) == 64
+    assert len(names) == 72 and len(set(names)) == 72
     assert set(names) == set(ops.REGISTRATIONS)
 
 

@@ -1,0 +1,256 @@
+"""Neural-network layers on the GPU against the CPU oracle, through the
+operator C-ABI (tp_amd_native_layer_norm, tp_amd_native_dropout,
+tp_amd_embedding, tp_amd_nll_loss and their backwards; the reference's
+NNKernels.cpp:57-395).
+
+Tolerances: the dropout mask and the embedding lookup are bit-exact (a
+mask decided by exact integer comparison, a row copy); the other results
+are float sums whose order differs from the oracle's, so they use the
+norm-wise rule of tests/_check.py (max |got - want| <= tol * 10 *
+max(max |want|, 1), tol 1e-5 float32, 2e-3 float16, 2e-2 bfloat16); the
+kept dropout values are within 1e-5 relative (float32) or one unit in the
+last place (16-bit).
+"""
+
+import importlib
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32, assert_bitexact, assert_elementwise, assert_normwise
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [F32, F16, BF16]
+IDS = ["fp32", "fp16", "bf16"]
+
+
+def tensor_mod():
+    return importlib.import_module("tensorplay-mlu_amd.tensor")
+
+
+def sample(orc, shape, dtype, seed=0, std=1.0, shift=0.0):
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+    return orc.from_float(x * np.float32(std) + np.float32(shift), dtype)
+
+
+# ---- layer norm ------------------------------------------------------------------
+
+LN_CASES = [
+    ((4, 16), (16,)),            # the reference test's case (tests/test_mlu.py:951)
+    ((3, 5, 24), (5, 24)),       # two normalized dimensions
+    ((300, 1024), (1024,)),      # packet rows, one wave
+    ((64, 4096), (4096,)),       # several waves per row
+    ((9, 1001), (1001,)),        # width not a whole number of packets
+    ((2, 40000), (40000,)),      # a row longer than the register-resident kernel holds
+]
+LN_IDS = ["4x16", "3x5x24", "300x1024", "64x4096", "9x1001", "2x40000"]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("shape,norm", LN_CASES, ids=LN_IDS)
+def test_layer_norm_forward(dev, ops, orc, dtype, shape, norm):
+    D = int(np.prod(norm))
+    x = sample(orc, shape, dtype, 1, 2.0, 0.5)
+    w = sample(orc, norm, dtype, 2)
+    b = sample(orc, norm, dtype, 3)
+    for affine in (True, False):
+        args = (dev.from_numpy(w, dtype=dtype), dev.from_numpy(b, dtype=dtype)) if affine else (None, None)
+        y, mean, rstd = ops.native_layer_norm(dev.from_numpy(x, dtype=dtype), norm, *args, eps=1e-5)
+        wy, wm, wr = orc.layer_norm(dtype, x, D, w if affine else None, b if affine else None, 1e-5)
+        assert y.shape == shape and mean.shape == (x.size // D,) and rstd.shape == mean.shape
+        what = f"{shape} affine={affine}"
+        assert_normwise(y.numpy(), wy, dtype, 1, "y " + what)
+        assert_normwise(mean.numpy(), wm, F32, 1, "mean " + what)
+        assert_normwise(rstd.numpy(), wr, F32, 1, "rstd " + what)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("shape,norm", LN_CASES, ids=LN_IDS)
+def test_layer_norm_backward(dev, ops, orc, dtype, shape, norm):
+    D = int(np.prod(norm))
+    rows = int(np.prod(shape)) // D
+    x = sample(orc, shape, dtype, 4, 1.5, -0.25)
+    w = sample(orc, norm, dtype, 5)
+    b = sample(orc, norm, dtype, 6)
+    dy = sample(orc, shape, dtype, 7)
+    dx_, w_, b_ = (dev.from_numpy(a, dtype=dtype) for a in (x, w, b))
+    _, mean, rstd = ops.native_layer_norm(dx_, norm, w_, b_, eps=1e-5)
+    m, r = mean.numpy(), rstd.numpy()
+    gx, gw, gb = ops.native_layer_norm_backward(dev.from_numpy(dy, dtype=dtype), dx_, norm, mean,
+                                                rstd, w_, b_)
+    ox, ow, ob = orc.layer_norm_backward(dtype, dy, x, D, m, r, w)
+    assert gx.shape == shape and gw.shape == tuple(norm) and gb.shape == tuple(norm)
+    assert_normwise(gx.numpy(), ox, dtype, 1, "dx")
+    # dW and dB sum over the rows
+    scale = max(1.0, np.sqrt(rows))
+    assert_normwise(gw.numpy().reshape(-1), ow, dtype, scale, "dweight")
+    assert_normwise(gb.numpy().reshape(-1), ob, dtype, scale, "dbias")
+    # without a weight, and with outputs masked off
+    gx2, gw2, gb2 = ops.native_layer_norm_backward(dev.from_numpy(dy, dtype=dtype), dx_, norm, mean,
+                                                   rstd, None, None, (True, False, True))
+    assert gw2 is None
+    ox2, _, ob2 = orc.layer_norm_backward(dtype, dy, x, D, m, r, None)
+    assert_normwise(gx2.numpy(), ox2, dtype, 1, "dx without weight")
+    assert_normwise(gb2.numpy().reshape(-1), ob2, dtype, scale, "dbias without weight")
+
+
+def test_layer_norm_strided_input_and_declines(dev, ops, orc):
+    a = sample(orc, (48, 32), F32, 8)
+    t = dev.from_numpy(a).t()  # [32, 48] view, not contiguous
+    y, mean, rstd = ops.native_layer_norm(t, (48,))
+    wy, _, _ = orc.layer_norm(F32, np.ascontiguousarray(a.T), 48)
+    assert_normwise(y.numpy(), wy, F32, 1, "transposed input")
+    DeclinedError = tensor_mod().DeclinedError
+    with pytest.raises(DeclinedError):
+        ops.native_layer_norm(dev.from_numpy(a), (48, 32))  # no outer dimension (:64)
+    with pytest.raises(DeclinedError):
+        ops.native_layer_norm(dev.from_numpy(a), (31,))  # shape mismatch (:67-68)
+    with pytest.raises(DeclinedError):
+        ops.native_layer_norm(dev.from_numpy(a.astype(np.float64)), (32,))  # not a native float
+
+
+# ---- dropout ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("p", [0.1, 0.5, 0.9])
+def test_dropout_matches_the_philox_stream(dev, ops, orc, dtype, p):
+    n = (1 << 20) + 3
+    x = sample(orc, (n,), dtype, 9)
+    seed = 0x5DEECE66D1234567
+    out, mask = ops.native_dropout(dev.from_numpy(x, dtype=dtype), p, True, seed)
+    wout, wmask = orc.dropout(dtype, x, p, seed, 0)
+    got_mask = mask.numpy()
+    assert got_mask.dtype == np.bool_
+    assert_bitexact(got_mask.astype(np.uint8), wmask, f"mask p={p}")
+    got = out.numpy()
+    keep = wmask.astype(bool)
+    assert_elementwise(got[keep], wout[keep], dtype, f"kept p={p}")
+    assert not got[~keep].view(np.uint8).any(), "dropped elements must be +0"
+
+
+def test_dropout_shapes_modes_and_backward(dev, ops, orc):
+    a = sample(orc, (37, 29), F32, 10)
+    d = dev.from_numpy(a)
+    # not training: the input unchanged, every element kept
+    out, mask = ops.native_dropout(d, 0.3, False, 1)
+    assert_bitexact(out.numpy(), a, "eval")
+    assert mask.numpy().all()
+    # p == 1 drops everything
+    out, mask = ops.native_dropout(d, 1.0, True, 1)
+    assert not out.numpy().any() and not mask.numpy().any()
+    # a strided view keeps its shape; the stream follows the logical order
+    t = d.t()
+    out, mask = ops.native_dropout(t, 0.5, None, 77)
+    wout, wmask = orc.dropout(F32, np.ascontiguousarray(a.T), 0.5, 77, 0)
+    assert out.shape == (29, 37) and mask.shape == (29, 37)
+    assert_bitexact(mask.numpy().astype(np.uint8), wmask, "strided mask")
+    # backward: grad * mask * scale
+    g = sample(orc, (29, 37), F32, 11)
+    for dtype in DTYPES:
+        gd = orc.from_float(orc.to_float(g, F32), dtype)
+        got = ops.native_dropout_backward(dev.from_numpy(gd, dtype=dtype), mask, 2.0).numpy()
+        want = orc.dropout_backward(dtype, gd, wmask, 2.0)
+        assert_bitexact(got, want, f"dropout backward dtype {dtype}")
+
+
+# ---- embedding -------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("dim", [768, 13], ids=["packets", "scalar"])
+@pytest.mark.parametrize("itype", [np.int64, np.int32], ids=["i64", "i32"])
+def test_embedding_lookup(dev, ops, orc, dtype, dim, itype):
+    V = 1000
+    w = sample(orc, (V, dim), dtype, 12)
+    idx = np.random.default_rng(13).integers(0, V, size=(4, 33)).astype(itype)
+    got = ops.embedding(dev.from_numpy(w, dtype=dtype), dev.from_numpy(idx)).numpy()
+    assert got.shape == (4, 33, dim)
+    assert_bitexact(got, orc.embedding(dtype, w, idx), "lookup")
+
+
+def test_embedding_out_of_range_rows_are_nan(dev, ops, orc):
+    w = sample(orc, (10, 64), F32, 14)
+    idx = np.array([2, 10, -1, 9], np.int64)
+    got = ops.embedding(dev.from_numpy(w), dev.from_numpy(idx)).numpy()
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all()
+    assert_bitexact(got[[0, 3]], w[[2, 9]], "valid rows")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("pad,freq", [(-1, False), (3, False), (3, True)],
+                         ids=["plain", "padding", "padding-freq"])
+def test_embedding_dense_backward(dev, ops, orc, dtype, pad, freq):
+    V, D = 50, 64
+    idx = np.random.default_rng(15).integers(0, V, size=(8, 33)).astype(np.int64)
+    idx[0, :5] = 3
+    dy = sample(orc, (8, 33, D), dtype, 16)
+    got = ops.embedding_dense_backward(dev.from_numpy(dy, dtype=dtype), dev.from_numpy(idx), V,
+                                       pad, freq).numpy()
+    want = orc.embedding_backward(dtype, dy, idx, V, pad, freq)
+    assert got.shape == (V, D)
+    counts = np.bincount(idx.reshape(-1), minlength=V)
+    assert_normwise(got, want, dtype, float(np.sqrt(counts.max())), "embedding backward")
+    if pad >= 0:
+        assert not orc.to_float(got[pad:pad + 1], dtype).any(), "padding row must stay zero"
+
+
+def test_embedding_declines_sparse(dev, ops, orc):
+    w = dev.from_numpy(sample(orc, (10, 8), F32, 17))
+    i = dev.from_numpy(np.array([1, 2], np.int64))
+    with pytest.raises(tensor_mod().DeclinedError):
+        ops.embedding(w, i, sparse=True)
+
+
+# ---- negative log-likelihood ------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("reduction", [0, 1, 2], ids=["none", "mean", "sum"])
+@pytest.mark.parametrize("weighted", [False, True], ids=["unweighted", "weighted"])
+def test_nll_loss(dev, ops, orc, dtype, reduction, weighted):
+    n, c = 1000, 37
+    x = sample(orc, (n, c), dtype, 18)
+    rng = np.random.default_rng(19)
+    t = rng.integers(0, c, size=n).astype(np.int64)
+    t[::17] = 5  # a custom ignore_index below
+    w = orc.from_float(rng.random(c).astype(np.float32) + 0.5, dtype) if weighted else None
+    dx_, dt_ = dev.from_numpy(x, dtype=dtype), dev.from_numpy(t)
+    dw_ = dev.from_numpy(w, dtype=dtype) if weighted else None
+    y, total = ops.nll_loss(dx_, dt_, dw_, reduction, 5)
+    wy, wtotal = orc.nll_loss(dtype, x, t, w, reduction, 5)
+    assert y.shape == wy.shape and total.shape == ()
+    assert_normwise(y.numpy(), wy, dtype, float(np.sqrt(n)) if reduction == 2 else 1, "loss")
+    assert_normwise(total.numpy(), wtotal, dtype, 1, "total weight")
+    g = sample(orc, (n,) if reduction == 0 else (), dtype, 20)
+    got = ops.nll_loss_backward(dev.from_numpy(g, dtype=dtype), dx_, dt_, dw_, reduction, 5,
+                                total).numpy()
+    want = orc.nll_loss_backward(dtype, g, (n, c), t, total.numpy(), w, reduction, 5)
+    assert_elementwise(got, want, dtype, "nll backward")
+
+
+def test_nll_loss_int32_targets_and_bad_target(dev, ops, orc):
+    x = sample(orc, (64, 10), F32, 21)
+    t = np.arange(64, dtype=np.int32) % 10
+    y, total = ops.nll_loss(dev.from_numpy(x), dev.from_numpy(t), None, 2, -100)
+    assert_normwise(y.numpy(), orc.nll_loss(F32, x, t, None, 2)[0], F32, 8, "int32 targets")
+    assert float(total.numpy()) == 64.0
+    t[7] = 10  # outside [0, C), not ignore_index
+    y, _ = ops.nll_loss(dev.from_numpy(x), dev.from_numpy(t), None, 0, -100)
+    got = y.numpy()
+    assert np.isnan(got[7]) and not np.isnan(np.delete(got, 7)).any()
+    dx = ops.nll_loss_backward(dev.from_numpy(np.ones(64, np.float32)), dev.from_numpy(x),
+                               dev.from_numpy(t), None, 0, -100,
+                               dev.from_numpy(np.zeros((), np.float32))).numpy()
+    assert np.isnan(dx[7]).all() and not np.isnan(np.delete(dx, 7, axis=0)).any()
+
+
+def test_nll_loss_large_batch(dev, ops, orc):
+    n, c = 2048, 32000
+    x = sample(orc, (n, c), F32, 22)
+    t = np.random.default_rng(23).integers(0, c, size=n).astype(np.int64)
+    dx_, dt_ = dev.from_numpy(x), dev.from_numpy(t)
+    y, total = ops.nll_loss(dx_, dt_, None, 1, -100)
+    assert_normwise(y.numpy(), orc.nll_loss(F32, x, t, None, 1)[0], F32, 1, "mean loss")
+    g = np.array(0.75, np.float32)
+    got = ops.nll_loss_backward(dev.from_numpy(g), dx_, dt_, None, 1, -100, total).numpy()
+    want = orc.nll_loss_backward(F32, g, (n, c), t, total.numpy(), None, 1, -100)
+    assert_elementwise(got, want, F32, "large nll backward")
