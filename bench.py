@@ -16,8 +16,9 @@ Also reported on the same line:
 * ``roofline``: the dominant kernel (the broadcasting binary kernel, float32
   add against a row-broadcast operand), its average launch duration from
   HIP events recorded on the library's own stream, against 8 TB/s;
-* ``suite``: per-kernel throughput of configs 2-5 (GB/s or TFLOP/s and the
-  fraction of the matching MI355X peak), each from HIP events;
+* ``suite``: per-kernel throughput of configs 2-5 and of the neural-network
+  layers (GB/s or TFLOP/s and the fraction of the matching MI355X peak), each
+  from HIP events;
 * ``cpu_baseline``: the repository's C oracle (a CPU port of the same
   operators, float64 arithmetic, OpenMP) timed on this host on a bounded
   sample of the same workload.
@@ -274,6 +275,65 @@ def suite_config5b(ops, dev, ev):
                               "flops_per_step": flops}}
 
 
+def suite_nn(ops, dev, ev):
+    """The neural-network layers next to the training step (the reference's
+    NNKernels.cpp): layer norm forward and backward over [8192, 4096] rows,
+    dropout p = 0.1 and its backward on [8192, 4096], an embedding lookup of
+    8192 indices into a [32000, 4096] table and its dense gradient, nll_loss
+    over [8192, 32000] log-probabilities and its backward.  GB/s of
+    algorithmic bytes (every input element read once, every output element
+    written once; the backward of the embedding writes the whole table)
+    against 8 TB/s."""
+    out = {}
+    g = np.random.default_rng(0)
+    rows, D, V, C = 8192, 4096, 32000, 32000
+
+    def put(shape, dtype, scale=1.0):
+        d = dev.from_numpy(g.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+        return d if dtype == F32 else ops.to(d, dtype)
+
+    def record(name, fn, nbytes, reps=10):
+        for _ in range(2):
+            fn()
+        ms = ev.time_ms(fn, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)}
+
+    idx = dev.from_numpy(g.integers(0, V, size=rows).astype(np.int64))
+    tgt = dev.from_numpy(g.integers(0, C, size=rows).astype(np.int64))
+    for dtype in (F32, BF16):
+        e, tag = ESIZE[dtype], NAME[dtype]
+        n = rows * D
+        x, dy = put((rows, D), dtype, 2.0), put((rows, D), dtype)
+        w, b = put((D,), dtype), put((D,), dtype)
+        _, mean, rstd = ops.native_layer_norm(x, (D,), w, b)
+        record(f"layer_norm_fwd_{rows}x{D}_{tag}", lambda: ops.native_layer_norm(x, (D,), w, b),
+               2 * n * e + 8 * rows)
+        record(f"layer_norm_bwd_{rows}x{D}_{tag}",
+               lambda: ops.native_layer_norm_backward(dy, x, (D,), mean, rstd, w, b), 3 * n * e + 8 * rows)
+        _, mask = ops.native_dropout(x, 0.1, True, 1)
+        record(f"dropout_{rows}x{D}_{tag}", lambda: ops.native_dropout(x, 0.1, True, 7), n * (2 * e + 1))
+        record(f"dropout_bwd_{rows}x{D}_{tag}", lambda: ops.native_dropout_backward(dy, mask, 1 / 0.9),
+               n * (2 * e + 1))
+        del x, mean, rstd, mask
+        table = put((V, D), dtype)
+        record(f"embedding_{rows}_from_{V}x{D}_{tag}", lambda: ops.embedding(table, idx),
+               2 * n * e + 8 * rows)
+        del table
+        record(f"embedding_bwd_{rows}_to_{V}x{D}_{tag}",
+               lambda: ops.embedding_dense_backward(dy, idx, V), n * e + V * D * e, reps=5)
+        del dy, w, b
+        logp = put((rows, C), dtype)
+        y, total = ops.nll_loss(logp, tgt, None, 1)
+        one = ops.to(dev.from_numpy(np.array(1.0, np.float32)), dtype)
+        record(f"nll_loss_{rows}x{C}_{tag}", lambda: ops.nll_loss(logp, tgt, None, 1), rows * (e + 8))
+        record(f"nll_loss_bwd_{rows}x{C}_{tag}",
+               lambda: ops.nll_loss_backward(one, logp, tgt, None, 1, -100, total), rows * C * e + rows * 8)
+        del logp, y, total
+    return out
+
+
 def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 8):
     """The C oracle (CPU port, float64 arithmetic, OpenMP over the host's
     cores) running the whole config-2 step -- all 8192 rows, both dtypes --
@@ -454,6 +514,8 @@ def main() -> int:
         suite["config4_5a"] = suite_gemm(ops, dev, ev)
         log("bench: suite config 5b")
         suite["config5b"] = suite_config5b(ops, dev, ev)
+        log("bench: suite NN layers")
+        suite["nn"] = suite_nn(ops, dev, ev)
         result["suite"] = suite
     if not args.no_cpu:
         log("bench: cpu baseline")

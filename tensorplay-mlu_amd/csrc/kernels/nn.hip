@@ -44,6 +44,56 @@ __device__ __forceinline__ float opaque(float v) {
     return v;
 }
 
+// ---- buffer access ------------------------------------------------------------
+//
+// The row kernels below address rows through buffer resources: a 16-byte
+// access past the resource's range is dropped by the hardware (a load gives
+// zeros), so a thread issues its loads and stores without a branch around
+// each, and the compiler can count the outstanding ones exactly -- it waits
+// for a prefetched row without also waiting for the stores issued after it.
+
+using Rsrc = __amdgpu_buffer_rsrc_t;
+typedef unsigned int U32x4 __attribute__((ext_vector_type(4)));
+constexpr int kNt = 2;  // cache policy: non-temporal
+
+// A resource over `bytes` bytes at `base`; 0 bytes makes every access out of
+// range (nothing is read or written).
+__device__ __forceinline__ Rsrc buffer_over(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(Rsrc r, uint32_t offset) {
+    const U32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kNt);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void buffer_store16(Rsrc r, uint32_t offset, const uint4& v) {
+    const U32x4 d = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(d, r, offset, 0, kNt);
+}
+
+__device__ __forceinline__ float buffer_load_f32(Rsrc r, uint32_t offset) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+}
+
+__device__ __forceinline__ void buffer_store_f32(Rsrc r, uint32_t offset, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, offset, 0, 0);
+}
+
+// A wave-uniform 64-bit value in scalar registers.
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+constexpr uint32_t kOutOfRange = 0xfffffff0u;  // an offset past any resource used here
+
+// Waits for every outstanding memory operation.  Before a software-pipelined
+// row loop this leaves nothing pending on entry, so the waits the compiler
+// places at the loop head follow the loop's own issue order alone.
+__device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
+
 // ---- layer norm -------------------------------------------------------------
 
 template <int WAVES>
@@ -85,7 +135,12 @@ __device__ __forceinline__ void load_params(const S_<T>* p, float (&out)[VPT][Pa
     }
 }
 
-// y = (x - mean) rstd w + b over rows of D (a multiple of the packet).
+// y = (x - mean) rstd w + b over rows of D (a multiple of the packet; a row
+// and the statistics arrays under 4 GiB).  A block holds kRows rows at a time
+// (WAVES waves each) and walks rows with stride gridDim.x kRows, two rows a
+// step in two register sets: the next row's packets are loaded before this
+// row's reductions, so the loads stay in flight across the barriers.  w and b
+// stay in registers as packets.
 template <typename T, int WAVES, int VPT>
 __global__ __launch_bounds__(ln_threads<WAVES>()) void layer_norm_rows_kernel(
     const S_<T>* x, const S_<T>* w, const S_<T>* b, S_<T>* y, float* mean_out, float* rstd_out,
@@ -95,58 +150,79 @@ __global__ __launch_bounds__(ln_threads<WAVES>()) void layer_norm_rows_kernel(
     constexpr int kRows = ln_threads<WAVES>() / kThreads;
     __shared__ float scratch[ln_threads<WAVES>() / kWave];
     const int tid = threadIdx.x % kThreads;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + threadIdx.x / kThreads;
-    const bool active = row < rows;
+    const int group = threadIdx.x / kThreads;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kRows;
+    const uint32_t row_bytes = static_cast<uint32_t>(D * sizeof(S_<T>));
     const int64_t npk = D / N;
-    float v[VPT][N];
-    float s = 0.0f;
+    const float inv_d = 1.0f / static_cast<float>(D);
+    const Rsrc stats_m = buffer_over(mean_out, static_cast<uint32_t>(rows * sizeof(float)));
+    const Rsrc stats_r = buffer_over(rstd_out, static_cast<uint32_t>(rows * sizeof(float)));
+    uint4 wr[VPT], br[VPT];
+    {
+        const Rsrc rw = buffer_over(w, w != nullptr ? row_bytes : 0);
+        const Rsrc rb = buffer_over(b, b != nullptr ? row_bytes : 0);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-        if (active && q < npk) {
-            unpack<T>(load_raw_nt(x + row * D + q * N), v[k]);
-#pragma unroll
-            for (int j = 0; j < N; ++j) s += v[k][j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) v[k][j] = 0.0f;
+        for (int k = 0; k < VPT; ++k) {
+            const uint32_t off = static_cast<uint32_t>(tid + k * kThreads) * 16u;
+            wr[k] = buffer_load16(rw, off);
+            br[k] = buffer_load16(rb, off);
         }
     }
-    const float inv_d = 1.0f / static_cast<float>(D);
-    const float mean = row_sum<WAVES>(s, scratch) * inv_d;
-    float ss = 0.0f;
+    auto fetch = [&](uint4 (&buf)[VPT], int64_t row) {
+        const Rsrc r = buffer_over(x + (row < rows ? row : 0) * D, row < rows ? row_bytes : 0);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-        if (active && q < npk) {
+        for (int k = 0; k < VPT; ++k) buf[k] = buffer_load16(r, static_cast<uint32_t>(tid + k * kThreads) * 16u);
+    };
+    auto process = [&](const uint4 (&buf)[VPT], int64_t row) {
+        float v[VPT][N];
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            unpack<T>(buf[k], v[k]);  // zeros past the row's end
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += v[k][j];
+        }
+        const float mean = row_sum<WAVES>(s, scratch) * inv_d;
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const bool in = tid + k * kThreads < npk;
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                const float d = v[k][j] - mean;
+                const float d = in ? v[k][j] - mean : 0.0f;
                 ss += d * d;
             }
         }
-    }
-    const float var = row_sum<WAVES>(ss, scratch) * inv_d;
-    const float rstd = 1.0f / sqrtf(var + eps);
-    if (!active) return;
+        const float var = row_sum<WAVES>(ss, scratch) * inv_d;
+        const float rstd = 1.0f / sqrtf(var + eps);
+        const bool active = row < rows;
+        const Rsrc ry = buffer_over(y + (active ? row : 0) * D, active ? row_bytes : 0);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-        if (q < npk) {
+        for (int k = 0; k < VPT; ++k) {
             float wv[N], bv[N], o[N];
-            if (w != nullptr) unpack<T>(*reinterpret_cast<const uint4*>(w + q * N), wv);
-            if (b != nullptr) unpack<T>(*reinterpret_cast<const uint4*>(b + q * N), bv);
+            unpack<T>(wr[k], wv);
+            unpack<T>(br[k], bv);
 #pragma unroll
             for (int j = 0; j < N; ++j) {
                 const float t = (v[k][j] - mean) * rstd;
                 o[j] = fmaf(t, w != nullptr ? wv[j] : 1.0f, b != nullptr ? bv[j] : 0.0f);
             }
-            store_raw_nt(y + row * D + q * N, pack<T>(o));
+            buffer_store16(ry, static_cast<uint32_t>(tid + k * kThreads) * 16u, pack<T>(o));
         }
-    }
-    if (tid == 0) {
-        mean_out[row] = mean;
-        rstd_out[row] = rstd;
+        const uint32_t stat_off = tid == 0 && active ? static_cast<uint32_t>(row) * 4u : kOutOfRange;
+        buffer_store_f32(stats_m, stat_off, mean);
+        buffer_store_f32(stats_r, stat_off, rstd);
+    };
+    uint4 a[VPT], bq[VPT];
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kRows;
+    fetch(a, uniform(first + group));
+    drain();
+    for (int64_t base = first; base < rows; base += 2 * stride) {
+        fetch(bq, uniform(base + stride + group));
+        process(a, uniform(base + group));
+        if (base + stride >= rows) break;
+        fetch(a, uniform(base + 2 * stride + group));
+        process(bq, uniform(base + stride + group));
     }
 }
 
@@ -181,79 +257,143 @@ __global__ __launch_bounds__(kBlock) void layer_norm_generic_kernel(
     }
 }
 
-// Backward over rows of D (a multiple of the packet).  Block b takes rows
-// b, b + gridDim.x, ...; per row
+// Backward over rows of D (a multiple of the packet; a row and the
+// statistics under 4 GiB).  A block is GROUPS row groups of WAVES waves; group
+// g of block b takes rows (b GROUPS + g) + i gridDim.x GROUPS.  Per row
 //   xhat = (x - mean) rstd,  g = dy w,
 //   dx = rstd (g - mean(g) - xhat mean(g xhat)),
-// and each thread adds dy xhat and dy into its columns' running sums, written
-// at the end as the block's float32 partial rows of dW and dB.
-template <typename T, int WAVES, int VPT>
-__global__ __launch_bounds__(WAVES * kWave) void layer_norm_backward_rows_kernel(
+// and each thread adds dy xhat and dy into its columns' running sums.  Rows
+// go two a step in two register sets of raw packets: the next row's x and dy
+// (and statistics) are loaded before this row's reductions, so the loads
+// stay in flight across the barriers; xhat and g are recomputed from the
+// packets for dx.  At the end the groups' running sums are added in order
+// through LDS (D floats of dynamic shared memory) into the block's float32
+// partial rows of dW and dB.
+template <typename T, int VPT>
+struct BwdRow {
+    uint4 x[VPT], d[VPT];
+    float mu, rs;
+};
+
+template <typename T, int WAVES, int VPT, int GROUPS>
+__global__ __launch_bounds__(GROUPS * WAVES * kWave) void layer_norm_backward_rows_kernel(
     const S_<T>* dy, const S_<T>* x, const float* mean, const float* rstd, const S_<T>* w,
     S_<T>* dx, float* dw_part, float* db_part, int64_t rows, int64_t D) {
     constexpr int N = Packet<T>::N;
     constexpr int kThreads = WAVES * kWave;
-    __shared__ float scratch[WAVES];
-    const int tid = threadIdx.x;
+    extern __shared__ float fold[];
+    __shared__ float scratch[GROUPS * WAVES];
+    const int tid = threadIdx.x % kThreads;
+    const int group = threadIdx.x / kThreads;
     const int64_t npk = D / N;
-    float wv[VPT][N], pw[VPT][N], pb[VPT][N];
-    load_params<T, VPT>(w, wv, tid, kThreads, npk, 1.0f);
+    const uint32_t row_bytes = static_cast<uint32_t>(D * sizeof(S_<T>));
+    const Rsrc rmean = buffer_over(mean, static_cast<uint32_t>(rows * sizeof(float)));
+    const Rsrc rrstd = buffer_over(rstd, static_cast<uint32_t>(rows * sizeof(float)));
+    uint4 wr[VPT];
+    {
+        const Rsrc rw = buffer_over(w, w != nullptr ? row_bytes : 0);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) wr[k] = buffer_load16(rw, static_cast<uint32_t>(tid + k * kThreads) * 16u);
+    }
+    float pw[VPT][N], pb[VPT][N];
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
 #pragma unroll
         for (int j = 0; j < N; ++j) pw[k][j] = pb[k][j] = 0.0f;
     const float inv_d = 1.0f / static_cast<float>(D);
-    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const float mu = mean[row], rs = rstd[row];
-        float xh[VPT][N], g[VPT][N];
+    // Row `row`'s packets and statistics (zeros past the last row).
+    auto fetch = [&](BwdRow<T, VPT>& buf, int64_t row) {
+        const bool ok = row < rows;
+        const int64_t at = (ok ? row : 0) * D;
+        const Rsrc rx = buffer_over(x + at, ok ? row_bytes : 0);
+        const Rsrc rd = buffer_over(dy + at, ok ? row_bytes : 0);
+        const uint32_t soff = ok ? static_cast<uint32_t>(row) * 4u : kOutOfRange;
+        buf.mu = buffer_load_f32(rmean, soff);
+        buf.rs = buffer_load_f32(rrstd, soff);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const uint32_t off = static_cast<uint32_t>(tid + k * kThreads) * 16u;
+            buf.x[k] = buffer_load16(rx, off);
+            buf.d[k] = buffer_load16(rd, off);
+        }
+    };
+    // xhat and g of packet k (zeros past the row's end).
+    auto terms = [&](const BwdRow<T, VPT>& buf, int k, float (&xh)[N], float (&g)[N], float (&dv)[N]) {
+        const bool in = tid + k * kThreads < npk;
+        float xv[N], wv[N];
+        unpack<T>(buf.x[k], xv);
+        unpack<T>(buf.d[k], dv);
+        unpack<T>(wr[k], wv);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            xh[j] = in ? (xv[j] - buf.mu) * buf.rs : 0.0f;
+            g[j] = dv[j] * (w != nullptr ? wv[j] : 1.0f);
+        }
+    };
+    auto process = [&](const BwdRow<T, VPT>& buf, int64_t row) {
         float a = 0.0f, c = 0.0f;
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
-            const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-            if (q < npk) {
-                float xv[N], dv[N];
-                unpack<T>(load_raw_nt(x + row * D + q * N), xv);
-                unpack<T>(load_raw_nt(dy + row * D + q * N), dv);
+            float xh[N], g[N], dv[N];
+            terms(buf, k, xh, g, dv);
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    xh[k][j] = (xv[j] - mu) * rs;
-                    g[k][j] = dv[j] * wv[k][j];
-                    a += g[k][j];
-                    c += g[k][j] * xh[k][j];
-                    pw[k][j] = fmaf(dv[j], xh[k][j], pw[k][j]);
-                    pb[k][j] += dv[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < N; ++j) xh[k][j] = g[k][j] = 0.0f;
+            for (int j = 0; j < N; ++j) {
+                a += g[j];
+                c += g[j] * xh[j];
+                pw[k][j] = fmaf(dv[j], xh[j], pw[k][j]);
+                pb[k][j] += dv[j];
             }
         }
         a = row_sum<WAVES>(a, scratch) * inv_d;
         c = row_sum<WAVES>(c, scratch) * inv_d;
-        if (dx != nullptr) {
-#pragma unroll
-            for (int k = 0; k < VPT; ++k) {
-                const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-                if (q < npk) {
-                    float o[N];
-#pragma unroll
-                    for (int j = 0; j < N; ++j) o[j] = rs * (g[k][j] - a - xh[k][j] * c);
-                    store_raw_nt(dx + row * D + q * N, pack<T>(o));
-                }
-            }
-        }
-    }
-    if (dw_part != nullptr) {
+        const bool write = dx != nullptr && row < rows;
+        const Rsrc rdx = buffer_over(dx + (write ? row * D : 0), write ? row_bytes : 0);
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
-            const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
-            if (q < npk) {
-                float* pwr = dw_part + static_cast<int64_t>(blockIdx.x) * D + q * N;
-                float* pbr = db_part + static_cast<int64_t>(blockIdx.x) * D + q * N;
+            float xh[N], g[N], dv[N], o[N];
+            terms(buf, k, xh, g, dv);
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    pwr[j] = pw[k][j];
-                    pbr[j] = pb[k][j];
+            for (int j = 0; j < N; ++j) o[j] = buf.rs * (g[j] - a - xh[j] * c);
+            buffer_store16(rdx, static_cast<uint32_t>(tid + k * kThreads) * 16u, pack<T>(o));
+        }
+    };
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * GROUPS;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * GROUPS;
+    BwdRow<T, VPT> ra, rb;
+    fetch(ra, uniform(first + group));
+    drain();
+    for (int64_t base = first; base < rows; base += 2 * step) {
+        fetch(rb, uniform(base + step + group));
+        process(ra, uniform(base + group));
+        if (base + step >= rows) break;
+        fetch(ra, uniform(base + 2 * step + group));
+        process(rb, uniform(base + step + group));
+    }
+    if (dw_part == nullptr) return;
+    // Groups 1 .. GROUPS-1 add into `fold` in turn, group 0 adds last and
+    // writes the block's partial row; dW then dB.
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        float (&mine)[VPT][N] = which == 0 ? pw : pb;
+        float* out = (which == 0 ? dw_part : db_part) + static_cast<int64_t>(blockIdx.x) * D;
+        for (int src = GROUPS - 1; src >= 0; --src) {
+            if constexpr (GROUPS > 1) __syncthreads();
+            if (group == src) {
+#pragma unroll
+                for (int k = 0; k < VPT; ++k) {
+                    const int64_t q = tid + static_cast<int64_t>(k) * kThreads;
+                    if (q < npk) {
+#pragma unroll
+                        for (int j = 0; j < N; ++j) {
+                            float v = mine[k][j];
+                            if (src < GROUPS - 1) v += fold[q * N + j];
+                            if (src > 0) {
+                                fold[q * N + j] = v;
+                            } else {
+                                out[q * N + j] = v;
+                            }
+                        }
+                    }
                 }
             }
         }
@@ -303,15 +443,83 @@ __global__ __launch_bounds__(kBlock) void layer_norm_param_grad_generic_kernel(
     db[j] = sb;
 }
 
-// Sum over `parts` float32 rows of D columns, in row order, rounded to T.
+// Sum over `parts` float32 rows of D columns, rounded to T: blockIdx.y picks
+// the matrix (0: part0 into out0, 1: part1 into out1; a null output is
+// skipped).  A block takes 4 kFoldQuads consecutive columns, a thread four
+// of them (one 16-byte load a row while the row holds four), in
+// kFoldThreads / kFoldQuads row groups; group g sums rows g, g + groups, ...
+// eight rows at a time into eight running sums (eight loads in flight), and
+// the sums and then the groups are added in a fixed order, so the result
+// does not depend on timing.
+constexpr int kFoldQuads = 16;
+constexpr int kFoldThreads = 1024;
+
 template <typename T>
-__global__ __launch_bounds__(kBlock) void fold_rows_kernel(const float* part, int64_t parts, int64_t D,
-                                                           S_<T>* out) {
-    const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (j >= D) return;
-    float s = 0.0f;
-    for (int64_t p = 0; p < parts; ++p) s += part[p * D + j];
-    out[j] = Elem<T>::store(s);
+__global__ __launch_bounds__(kFoldThreads) void fold_rows_kernel(const float* part0, const float* part1,
+                                                                 int64_t parts, int64_t D, S_<T>* out0,
+                                                                 S_<T>* out1) {
+    constexpr int kGroups = kFoldThreads / kFoldQuads;
+    __shared__ float4 sums[kGroups][kFoldQuads];
+    const float* part = blockIdx.y == 0 ? part0 : part1;
+    S_<T>* out = blockIdx.y == 0 ? out0 : out1;
+    if (out == nullptr) return;
+    const int quad = threadIdx.x % kFoldQuads, grp = threadIdx.x / kFoldQuads;
+    const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * kFoldQuads + quad) * 4;
+    const bool whole = j0 + 4 <= D && (D & 3) == 0;
+    constexpr int kLanes = 8;
+    float acc[kLanes][4];
+#pragma unroll
+    for (int l = 0; l < kLanes; ++l) acc[l][0] = acc[l][1] = acc[l][2] = acc[l][3] = 0.0f;
+    auto add_row = [&](int64_t p, float (&acc)[4]) {
+        if (whole) {
+            const float4 v = *reinterpret_cast<const float4*>(part + p * D + j0);
+            acc[0] += v.x;
+            acc[1] += v.y;
+            acc[2] += v.z;
+            acc[3] += v.w;
+        } else {
+            for (int k = 0; k < 4; ++k) {
+                if (j0 + k < D) acc[k] += part[p * D + j0 + k];
+            }
+        }
+    };
+    int64_t p = grp;
+    for (; p + (kLanes - 1) * kGroups < parts; p += kLanes * kGroups) {
+#pragma unroll
+        for (int l = 0; l < kLanes; ++l) add_row(p + l * kGroups, acc[l]);
+    }
+    for (; p < parts; p += kGroups) add_row(p, acc[0]);
+#pragma unroll
+    for (int l = 1; l < kLanes; ++l) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[0][k] += acc[l][k];
+    }
+    sums[grp][quad] = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+    // pairwise tree over the groups
+#pragma unroll
+    for (int h = kGroups / 2; h >= 1; h /= 2) {
+        __syncthreads();
+        if (grp < h) {
+            const float4 u = sums[grp + h][quad];
+            float4& t = sums[grp][quad];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+    }
+    __syncthreads();
+    if (grp == 0) {
+        const float4 t = sums[0][quad];
+        const float r[4] = {t.x, t.y, t.z, t.w};
+        for (int k = 0; k < 4; ++k) {
+            if (j0 + k < D) out[j0 + k] = Elem<T>::store(r[k]);
+        }
+    }
+}
+
+inline dim3 fold_grid(int64_t D) {
+    return dim3(static_cast<uint32_t>((D + 4 * kFoldQuads - 1) / (4 * kFoldQuads)), 2);
 }
 
 struct RowShape {
@@ -332,13 +540,32 @@ RowShape row_shape(int64_t npk, int max_vpt) {
     return RowShape{};
 }
 
-// The forward holds up to 4 packets a thread; the backward, which keeps five
-// float arrays per thread, 4 of float32 and 2 of a 16-bit type.
+// The backward's shape: 8 elements a thread (fp32 2 packets, 16-bit 1) on
+// the fewest waves, up to 16, that hold the row.
+constexpr int bwd_vpt(int elems) { return 8 / elems; }
+
+RowShape backward_row_shape(int64_t npk, int elems) {
+    const int vpt = bwd_vpt(elems);
+    for (int waves : {1, 2, 4, 8, 16}) {
+        if (static_cast<int64_t>(waves) * kWave * vpt >= npk) return RowShape{waves, vpt};
+    }
+    return RowShape{};
+}
+
+// The forward holds up to 4 packets a thread.
 #define TP_AMD_LN_SHAPES(X) \
     X(1, 1) X(1, 2) X(1, 4) X(2, 2) X(2, 4) X(4, 2) X(4, 4) X(8, 2) X(8, 4) X(16, 2) X(16, 4)
-template <typename T>
-constexpr int bwd_max_vpt() {
-    return Packet<T>::N == 4 ? 4 : 2;
+// Waves a row in the backward; a block holds 16 waves in 16 / W row groups.
+#define TP_AMD_LN_BWD_SHAPES(X) X(1) X(2) X(4) X(8) X(16)
+
+// Blocks of `kernel` the GPU holds at once (its occupancy per CU times the
+// CUs), at most `work`.
+template <typename K>
+int64_t resident_grid(K kernel, int threads, int device, int64_t work, size_t lds = 0) {
+    int per_cu = 0;
+    TP_AMD_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds));
+    const int64_t grid = static_cast<int64_t>(cu_count(device)) * (per_cu > 0 ? per_cu : 1);
+    return grid < work ? grid : work;
 }
 
 template <typename T>
@@ -351,14 +578,16 @@ void layer_norm_typed(int device, int64_t rows, int64_t D, const void* xv, const
     const S* b = static_cast<const S*>(bv);
     S* y = static_cast<S*>(yv);
     hipStream_t st = stream(device);
-    const bool vec = D % N == 0 && aligned16(x) && aligned16(y) && (w == nullptr || aligned16(w)) &&
-                     (b == nullptr || aligned16(b));
+    // The row kernels address rows and the statistics with 32-bit byte offsets.
+    const bool vec = D % N == 0 && rows < (int64_t{1} << 30) && aligned16(x) && aligned16(y) &&
+                     (w == nullptr || aligned16(w)) && (b == nullptr || aligned16(b));
     const RowShape rs = vec ? row_shape(D / N, 4) : RowShape{};
 #define TP_AMD_LN_FWD(W, V)                                                                      \
     if constexpr (W == 1 || V == 4) {                                                            \
         if (rs.waves == W && rs.vpt == V) {                                                      \
             constexpr int kRows = ln_threads<W>() / (W * kWave);                                 \
-            const int64_t blocks = (rows + kRows - 1) / kRows;                                   \
+            const int64_t blocks = resident_grid(layer_norm_rows_kernel<T, W, V>, ln_threads<W>(), \
+                                                 device, (rows + kRows - 1) / kRows);            \
             layer_norm_rows_kernel<T, W, V><<<blocks, ln_threads<W>(), 0, st>>>(                 \
                 x, w, b, y, mean, rstd, rows, D, eps);                                           \
             TP_AMD_HIP_CHECK(hipGetLastError());                                                 \
@@ -383,36 +612,35 @@ void layer_norm_backward_typed(int device, int64_t rows, int64_t D, const void* 
     S* dx = static_cast<S*>(dxv);
     hipStream_t st = stream(device);
     const bool params = dwv != nullptr || dbv != nullptr;
-    const bool vec = D % N == 0 && aligned16(x) && aligned16(dy) && (dx == nullptr || aligned16(dx)) &&
-                     (w == nullptr || aligned16(w));
-    const RowShape shape = vec ? row_shape(D / N, bwd_max_vpt<T>()) : RowShape{};
+    // The row kernels address rows and the statistics with 32-bit byte offsets.
+    const bool vec = D % N == 0 && rows < (int64_t{1} << 30) && aligned16(x) && aligned16(dy) &&
+                     (dx == nullptr || aligned16(dx)) && (w == nullptr || aligned16(w));
+    const RowShape shape = vec ? backward_row_shape(D / N, N) : RowShape{};
     if (shape.waves > 0) {
-        // A few blocks per CU walk the rows; each leaves one partial row of
-        // dW and of dB.
-        const int64_t per_cu = shape.waves >= 4 ? 2 : 8;
-        int64_t grid = static_cast<int64_t>(cu_count(device)) * per_cu;
-        if (grid > rows) grid = rows;
-        Workspace ws(params ? static_cast<size_t>(2 * grid * D) * sizeof(float) : 0, device);
-        float* dw_part = params ? static_cast<float*>(ws.get()) : nullptr;
-        float* db_part = params ? dw_part + grid * D : nullptr;
-#define TP_AMD_LN_BWD(W, V)                                                                    \
-    if constexpr (V <= bwd_max_vpt<T>() && (W == 1 || V == bwd_max_vpt<T>())) {                \
-        if (shape.waves == W && shape.vpt == V) {                                              \
-            layer_norm_backward_rows_kernel<T, W, V><<<grid, W * kWave, 0, st>>>(              \
-                dy, x, mean, rstd, w, dx, dw_part, db_part, rows, D);                          \
-        }                                                                                      \
-    }
-        TP_AMD_LN_SHAPES(TP_AMD_LN_BWD)
+        // As many blocks as the GPU holds at once walk the rows; each leaves
+        // one partial row of dW and of dB.
+        int64_t grid = 0;
+        Workspace ws;
+        float *dw_part = nullptr, *db_part = nullptr;
+        auto launch = [&](auto kernel, int groups, int threads) {
+            const size_t lds = groups > 1 ? static_cast<size_t>(D) * sizeof(float) : 0;
+            grid = resident_grid(kernel, threads, device, (rows + groups - 1) / groups, lds);
+            if (params) {
+                ws = Workspace(static_cast<size_t>(2 * grid * D) * sizeof(float), device);
+                dw_part = static_cast<float*>(ws.get());
+                db_part = dw_part + grid * D;
+            }
+            kernel<<<grid, threads, lds, st>>>(dy, x, mean, rstd, w, dx, dw_part, db_part, rows, D);
+        };
+        constexpr int V = bwd_vpt(N);
+#define TP_AMD_LN_BWD(W)                                                                             \
+    if (shape.waves == W) launch(layer_norm_backward_rows_kernel<T, W, V, 16 / W>, 16 / W, 16 * kWave);
+        TP_AMD_LN_BWD_SHAPES(TP_AMD_LN_BWD)
 #undef TP_AMD_LN_BWD
         TP_AMD_HIP_CHECK(hipGetLastError());
         if (params) {
-            const int64_t blocks = (D + kBlock - 1) / kBlock;
-            Workspace tmp;
-            if (dwv == nullptr || dbv == nullptr) tmp = Workspace(static_cast<size_t>(D) * sizeof(S), device);
-            fold_rows_kernel<T><<<blocks, kBlock, 0, st>>>(dw_part, grid, D,
-                                                           static_cast<S*>(dwv ? dwv : tmp.get()));
-            fold_rows_kernel<T><<<blocks, kBlock, 0, st>>>(db_part, grid, D,
-                                                           static_cast<S*>(dbv ? dbv : tmp.get()));
+            fold_rows_kernel<T><<<fold_grid(D), kFoldThreads, 0, st>>>(dw_part, db_part, grid, D, static_cast<S*>(dwv),
+                                                              static_cast<S*>(dbv));
             TP_AMD_HIP_CHECK(hipGetLastError());
         }
         return;
@@ -428,10 +656,8 @@ void layer_norm_backward_typed(int device, int64_t rows, int64_t D, const void* 
         const int64_t blocks = (D + kBlock - 1) / kBlock;
         layer_norm_param_grad_generic_kernel<T><<<blocks, kBlock, 0, st>>>(dy, x, mean, rstd, dwf, dbf,
                                                                            rows, D);
-        Workspace tmp;
-        if (dwv == nullptr || dbv == nullptr) tmp = Workspace(static_cast<size_t>(D) * sizeof(S), device);
-        fold_rows_kernel<T><<<blocks, kBlock, 0, st>>>(dwf, 1, D, static_cast<S*>(dwv ? dwv : tmp.get()));
-        fold_rows_kernel<T><<<blocks, kBlock, 0, st>>>(dbf, 1, D, static_cast<S*>(dbv ? dbv : tmp.get()));
+        fold_rows_kernel<T><<<fold_grid(D), kFoldThreads, 0, st>>>(dwf, dbf, 1, D, static_cast<S*>(dwv),
+                                                          static_cast<S*>(dbv));
         TP_AMD_HIP_CHECK(hipGetLastError());
     }
 }
@@ -470,55 +696,98 @@ __device__ __forceinline__ Philox philox4x32_10(uint32_t c0, uint32_t c1, uint32
     return Philox{{c0, c1, c2, c3}};
 }
 
-// Four elements per thread (one Philox block): out = keep ? x * scale : 0,
-// mask = keep.
+// The keep bits of Philox blocks b0 .. b0 + NB - 1, four elements each.
+template <int NB>
+__device__ __forceinline__ void keep_bits(int64_t b0, uint32_t threshold, uint32_t k0, uint32_t k1,
+                                          uint32_t off0, uint32_t off1, uint8_t (&m)[4 * NB]) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint64_t blk = static_cast<uint64_t>(b0 + b);
+        const Philox r = philox4x32_10(static_cast<uint32_t>(blk), static_cast<uint32_t>(blk >> 32), off0,
+                                       off1, k0, k1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m[4 * b + j] = (r.c[j] >> 8) >= threshold ? 1 : 0;
+    }
+}
+
+// N mask bytes (4 or 8) as one store; the address is a multiple of N.
+template <int N>
+__device__ __forceinline__ void store_mask(uint8_t* p, const uint8_t (&m)[N]) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lo |= static_cast<uint32_t>(m[j]) << (8 * j);
+    if constexpr (N == 8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hi |= static_cast<uint32_t>(m[4 + j]) << (8 * j);
+        *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+    } else {
+        *reinterpret_cast<uint32_t*>(p) = lo;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void load_mask(const uint8_t* p, float (&m)[N]) {
+    uint32_t w[N / 4];
+    if constexpr (N == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        w[0] = v.x;
+        w[1] = v.y;
+    } else {
+        w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) m[j] = ((w[j / 4] >> (8 * (j % 4))) & 0xffu) != 0 ? 1.0f : 0.0f;
+}
+
+// One 16-byte packet per thread (4 float32 or 8 16-bit elements, one or two
+// Philox blocks): out = keep ? x * scale : 0, mask = keep.  `vec` says x and
+// out are 16-byte aligned; elements past the last whole packet, or all of
+// them without `vec`, go one at a time.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void dropout_kernel(const S_<T>* x, S_<T>* out, uint8_t* mask,
                                                          int64_t n, uint32_t threshold, float scale,
                                                          uint32_t k0, uint32_t k1, uint32_t off0,
-                                                         uint32_t off1) {
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;  // Philox block
-    const int64_t e0 = g * 4;
+                                                         uint32_t off1, bool vec) {
+    constexpr int N = Packet<T>::N;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t e0 = t * N;
     if (e0 >= n) return;
-    const Philox r = philox4x32_10(static_cast<uint32_t>(g), static_cast<uint32_t>(g >> 32), off0, off1,
-                                   k0, k1);
-    const bool full = e0 + 4 <= n;
-    uint8_t m[4];
-    float xv[4];
+    uint8_t m[N];
+    keep_bits<N / 4>(t * (N / 4), threshold, k0, k1, off0, off1, m);
+    if (vec && e0 + N <= n) {
+        float xv[N], o[N];
+        unpack<T>(load_raw_nt(x + e0), xv);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        m[j] = (r.c[j] >> 8) >= threshold ? 1 : 0;
-        xv[j] = (full || e0 + j < n) ? Elem<T>::load(x[e0 + j]) : 0.0f;
-    }
-    if (full) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[e0 + j] = Elem<T>::store(m[j] ? opaque(xv[j] * scale) : 0.0f);
-        uint32_t packed = m[0] | (m[1] << 8) | (m[2] << 16) | (static_cast<uint32_t>(m[3]) << 24);
-        if ((reinterpret_cast<uintptr_t>(mask + e0) & 3u) == 0) {
-            *reinterpret_cast<uint32_t*>(mask + e0) = packed;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) mask[e0 + j] = m[j];
-        }
+        for (int j = 0; j < N; ++j) o[j] = m[j] ? opaque(xv[j] * scale) : 0.0f;
+        store_raw_nt(out + e0, pack<T>(o));
+        store_mask<N>(mask + e0, m);
     } else {
-        for (int j = 0; j < 4 && e0 + j < n; ++j) {
-            out[e0 + j] = Elem<T>::store(m[j] ? opaque(xv[j] * scale) : 0.0f);
+        for (int j = 0; j < N && e0 + j < n; ++j) {
+            out[e0 + j] = Elem<T>::store(m[j] ? opaque(Elem<T>::load(x[e0 + j]) * scale) : 0.0f);
             mask[e0 + j] = m[j];
         }
     }
 }
 
-// out = grad * mask * scale (mask bytes 0 / 1).
+// out = grad * mask * scale (mask bytes 0 / 1), one packet per thread.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void dropout_backward_kernel(const S_<T>* grad, const uint8_t* mask,
-                                                                  S_<T>* out, int64_t n, float scale) {
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 4;
+                                                                  S_<T>* out, int64_t n, float scale,
+                                                                  bool vec) {
+    constexpr int N = Packet<T>::N;
+    const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * N;
+    if (e0 >= n) return;
+    if (vec && e0 + N <= n) {
+        float g[N], m[N], o[N];
+        unpack<T>(load_raw_nt(grad + e0), g);
+        load_mask<N>(mask + e0, m);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int64_t i = i0 + j;
-        if (i < n) {
-            const float m = mask[i] != 0 ? 1.0f : 0.0f;
-            out[i] = Elem<T>::store(opaque(Elem<T>::load(grad[i]) * m * scale));
+        for (int j = 0; j < N; ++j) o[j] = opaque(g[j] * m[j] * scale);
+        store_raw_nt(out + e0, pack<T>(o));
+    } else {
+        for (int j = 0; j < N && e0 + j < n; ++j) {
+            const float m = mask[e0 + j] != 0 ? 1.0f : 0.0f;
+            out[e0 + j] = Elem<T>::store(opaque(Elem<T>::load(grad[e0 + j]) * m * scale));
         }
     }
 }
@@ -561,6 +830,12 @@ __global__ __launch_bounds__(kBlock) void embedding_kernel(const S_<T>* weight, 
     }
 }
 
+// The dense gradient gathers instead of scattering: the samples of each
+// table row are listed (count, exclusive scan, fill), then one block per row
+// writes the row once -- the sum of its samples' dy rows in increasing
+// sample order, or zeros -- so the whole table is written exactly once and
+// the result does not depend on timing.
+
 // counts[idx[i]] += 1 for valid, non-padding indices.
 template <typename I>
 __global__ __launch_bounds__(kBlock) void embedding_count_kernel(const void* idx, int64_t n, int64_t V,
@@ -571,21 +846,171 @@ __global__ __launch_bounds__(kBlock) void embedding_count_kernel(const void* idx
     if (r >= 0 && r < V && r != padding_idx) atomicAdd(&counts[r], 1);
 }
 
-// acc[idx[i], :] += dy[i, :] (divided by the index's count with
-// scale_grad_by_freq); a wave per index, float32 atomics.
-template <typename T, typename I>
-__global__ __launch_bounds__(kBlock) void embedding_backward_kernel(const S_<T>* dy, const void* idx,
-                                                                    int64_t n, int64_t V, int64_t D,
-                                                                    int64_t padding_idx,
-                                                                    const int* counts, float* acc) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
+constexpr int kScanThreads = 1024;
+constexpr int kScanPer = 16;  // counts per lane in a tile
+
+// Inclusive prefix sum across the 64 lanes with DPP lane moves: shifts by
+// 1, 2, 4 and 8 within each row of 16 lanes (a lane with no source adds 0),
+// then lane 15 of rows 0 and 2 added to rows 1 and 3, then lane 31 to rows 2
+// and 3.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
+    return v;
+}
+
+// offsets[0 .. V] = exclusive scan of counts[0 .. V), and counts zeroed (they
+// become the fill cursors).  One block walks tiles of kScanThreads x
+// kScanPer counts; wave w owns the tile's w-th run of kWave x kScanPer
+// counts and reads it kWave at a time (lane l takes run index k kWave + l,
+// so every access is one coalesced line), scanning each step across the
+// wave; the waves' totals are scanned across the block and a carry moves to
+// the next tile.
+__global__ __launch_bounds__(kScanThreads) void embedding_scan_kernel(int* counts, int* offsets, int64_t V) {
+    __shared__ int wave_tot[kScanThreads / kWave];
+    __shared__ int carry_s;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    if (threadIdx.x == 0) carry_s = 0;
+    constexpr int64_t kRun = static_cast<int64_t>(kWave) * kScanPer;
+    constexpr int64_t kTile = kRun * (kScanThreads / kWave);
+    for (int64_t base = 0; base < V; base += kTile) {
+        const int64_t run0 = base + wave * kRun;
+        int v[kScanPer];
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int64_t r = run0 + k * kWave + lane;
+            v[k] = r < V ? counts[r] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) v[k] = wave_inclusive_scan(v[k]);
+        int total = 0;
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int step_total = __builtin_amdgcn_readlane(v[k], kWave - 1);
+            v[k] += total;  // inclusive prefix within the wave's run
+            total += step_total;
+        }
+        __syncthreads();  // carry_s and wave_tot of the previous tile are read
+        if (lane == 0) wave_tot[wave] = total;
+        __syncthreads();
+        int before = carry_s;
+        for (int w = 0; w < wave; ++w) before += wave_tot[w];
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int64_t r = run0 + k * kWave + lane;
+            if (r < V) {
+                offsets[r + 1] = before + v[k];
+                counts[r] = 0;
+            }
+        }
+        __syncthreads();  // everyone has read carry_s
+        if (threadIdx.x == kScanThreads - 1) carry_s = before + total;
+    }
+    if (threadIdx.x == 0) offsets[0] = 0;
+}
+
+// list[offsets[r] + k] = i, k the arrival order among row r's samples.
+template <typename I>
+__global__ __launch_bounds__(kBlock) void embedding_fill_kernel(const void* idx, int64_t n, int64_t V,
+                                                                int64_t padding_idx, const int* offsets,
+                                                                int* cursors, int* list) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n) return;
     const int64_t r = index_at<I>(idx, i);
-    if (r < 0 || r >= V || r == padding_idx) return;
-    const float scale = counts != nullptr ? 1.0f / static_cast<float>(counts[r]) : 1.0f;
-    for (int64_t q = lane; q < D; q += kWave) {
-        atomicAdd(&acc[r * D + q], Elem<T>::load(dy[i * D + q]) * scale);
+    if (r >= 0 && r < V && r != padding_idx) {
+        const int64_t pos = static_cast<int64_t>(offsets[r]) + atomicAdd(&cursors[r], 1);
+        if (pos < n) list[pos] = static_cast<int>(i);  // always true; keeps the write inside `list`
+    }
+}
+
+constexpr int kSortCap = 2048;  // samples of one row ordered in LDS; more go through `sorted`
+
+// Row r of the gradient (one block): the samples listed for r put in
+// increasing order (each entry's rank among the row's entries, the entries
+// being distinct), then each thread sums its columns over them in that
+// order, scaled by 1 / count with scale_grad_by_freq.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void embedding_gather_kernel(const S_<T>* dy, const int* offsets,
+                                                                  const int* list, int* sorted, int n_list,
+                                                                  int64_t D, int scale_grad_by_freq,
+                                                                  S_<T>* out) {
+    constexpr int N = VEC ? Packet<T>::N : 1;
+    __shared__ int stage[kSortCap];
+    __shared__ int order[kSortCap];
+    const int64_t r = blockIdx.x;
+    // offsets rise from 0 to at most n; the clamps keep reads inside `list`
+    const int off = max(offsets[r], 0);
+    const int c = max(0, min(offsets[r + 1], n_list) - off);
+    const int64_t units = D / N;
+    S_<T>* row = out + r * D;
+    if (c == 0) {
+        for (int64_t q = threadIdx.x; q < units; q += kBlock) {
+            if constexpr (VEC) {
+                store_raw_nt(row + q * N, make_uint4(0u, 0u, 0u, 0u));
+            } else {
+                row[q] = Elem<T>::store(0.0f);
+            }
+        }
+        return;
+    }
+    const int* entries;
+    if (c <= kSortCap) {
+        for (int u = threadIdx.x; u < c; u += kBlock) stage[u] = list[off + u];
+        __syncthreads();
+        for (int u = threadIdx.x; u < c; u += kBlock) {
+            const int e = stage[u];
+            int rank = 0;
+            for (int v = 0; v < c; ++v) rank += stage[v] < e;
+            order[rank] = e;
+        }
+        __syncthreads();
+        entries = order;
+    } else {
+        // Rank against the list in chunks staged through LDS; the ordered
+        // entries go to this row's range of `sorted`.
+        for (int u0 = 0; u0 < c; u0 += kBlock) {
+            const int u = u0 + threadIdx.x;
+            const int e = u < c ? list[off + u] : 0;
+            int rank = 0;
+            for (int v0 = 0; v0 < c; v0 += kSortCap) {
+                const int len = c - v0 < kSortCap ? c - v0 : kSortCap;
+                __syncthreads();
+                for (int v = threadIdx.x; v < len; v += kBlock) stage[v] = list[off + v0 + v];
+                __syncthreads();
+                for (int v = 0; v < len; ++v) rank += stage[v] < e;
+            }
+            if (u < c) sorted[off + rank] = e;
+        }
+        __syncthreads();
+        entries = sorted + off;
+    }
+    const float scale = scale_grad_by_freq ? 1.0f / static_cast<float>(c) : 1.0f;
+    for (int64_t q = threadIdx.x; q < units; q += kBlock) {
+        float acc[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[j] = 0.0f;
+        for (int k = 0; k < c; ++k) {
+            const int64_t e = entries[k];
+            if constexpr (VEC) {
+                float v[N];
+                unpack<T>(load_raw_nt(dy + e * D + q * N), v);
+#pragma unroll
+                for (int j = 0; j < N; ++j) acc[j] += v[j];
+            } else {
+                acc[0] += Elem<T>::load(dy[e * D + q]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[j] *= scale;
+        if constexpr (VEC) {
+            store_raw_nt(row + q * N, pack<T>(acc));
+        } else {
+            row[q] = Elem<T>::store(acc[0]);
+        }
     }
 }
 
@@ -686,6 +1111,36 @@ __global__ __launch_bounds__(kBlock) void nll_backward_kernel(const S_<T>* grad,
     dx[e] = Elem<T>::store(opaque(v));
 }
 
+// The same with dx as rows of 16-byte packets (C a multiple of the packet,
+// dx aligned): a row takes `blocks_per_row` blocks, each thread one packet,
+// holding the target's value if the target falls inside it.
+template <typename T, typename I>
+__global__ __launch_bounds__(kBlock) void nll_backward_rows_kernel(const S_<T>* grad, const void* target,
+                                                                   const S_<T>* w, const S_<T>* total,
+                                                                   int64_t C, uint32_t blocks_per_row,
+                                                                   int64_t ignore_index, int reduction,
+                                                                   S_<T>* dx) {
+    constexpr int N = Packet<T>::N;
+    const uint32_t i = blockIdx.x / blocks_per_row;
+    const int64_t q = static_cast<int64_t>(blockIdx.x - i * blocks_per_row) * kBlock + threadIdx.x;
+    if (q >= C / N) return;
+    const int64_t t = index_at<I>(target, i);
+    const bool bad = t != ignore_index && (t < 0 || t >= C);
+    float v[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = bad ? __builtin_nanf("") : 0.0f;
+    const int64_t k = t - q * N;
+    if (!bad && t != ignore_index && k >= 0 && k < N) {
+        const float g = reduction == 0 ? Elem<T>::load(grad[i])
+                        : reduction == 1 ? Elem<T>::load(grad[0]) / Elem<T>::load(total[0])
+                                         : Elem<T>::load(grad[0]);
+        const float val = opaque(-(w != nullptr ? Elem<T>::load(w[t]) : 1.0f) * g);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = j == k ? val : v[j];
+    }
+    store_raw_nt(dx + static_cast<int64_t>(i) * C + q * N, pack<T>(v));
+}
+
 template <typename T, typename F>
 void dispatch_index(int index_dtype, F&& f) {
     if (index_dtype == TP_AMD_INT64) {
@@ -771,12 +1226,13 @@ int tp_amd_launch_dropout(int device, int dtype, int64_t n, const void* x, doubl
         // p 2^24 is exact in double; a 24-bit uniform u 2^-24 is >= p exactly
         // when u >= ceil(p 2^24) (at most 2^24, which keeps nothing).
         const uint32_t threshold = static_cast<uint32_t>(std::ceil(std::ldexp(p, 24)));
-        const int64_t blocks = blocks_for((n + 3) / 4, kBlock);
         TP_AMD_DISPATCH_NN(dtype, T, {
-            dropout_kernel<T><<<blocks, kBlock, 0, stream(index)>>>(
+            constexpr int N = Packet<T>::N;
+            const bool vec = aligned16(x) && aligned16(out) && reinterpret_cast<uintptr_t>(mask) % N == 0;
+            dropout_kernel<T><<<blocks_for((n + N - 1) / N, kBlock), kBlock, 0, stream(index)>>>(
                 static_cast<const S_<T>*>(x), static_cast<S_<T>*>(out), mask, n, threshold, scale,
                 static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32),
-                static_cast<uint32_t>(offset), static_cast<uint32_t>(offset >> 32));
+                static_cast<uint32_t>(offset), static_cast<uint32_t>(offset >> 32), vec);
         });
         TP_AMD_HIP_CHECK(hipGetLastError());
     });
@@ -789,11 +1245,12 @@ int tp_amd_launch_dropout_backward(int device, int dtype, int64_t n, const void*
         if (n == 0) return;
         const int index = resolve_device(device);
         DeviceGuard guard(index);
-        const int64_t blocks = blocks_for((n + 3) / 4, kBlock);
         TP_AMD_DISPATCH_NN(dtype, T, {
-            dropout_backward_kernel<T><<<blocks, kBlock, 0, stream(index)>>>(
+            constexpr int N = Packet<T>::N;
+            const bool vec = aligned16(grad) && aligned16(out) && reinterpret_cast<uintptr_t>(mask) % N == 0;
+            dropout_backward_kernel<T><<<blocks_for((n + N - 1) / N, kBlock), kBlock, 0, stream(index)>>>(
                 static_cast<const S_<T>*>(grad), mask, static_cast<S_<T>*>(out), n,
-                static_cast<float>(scale));
+                static_cast<float>(scale), vec);
         });
         TP_AMD_HIP_CHECK(hipGetLastError());
     });
@@ -832,36 +1289,45 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
     return guarded([&] {
         TP_AMD_CHECK(num_weights >= 0 && dim >= 0 && n >= 0, "embedding_backward: negative extent");
         if (num_weights == 0 || dim == 0) return;
+        TP_AMD_CHECK(n < 0x7fffffff && num_weights < 0x7fffffff,
+                     "embedding_backward: at most 2^31 - 2 samples and table rows");
         const int index = resolve_device(device);
         DeviceGuard guard(index);
         hipStream_t st = stream(index);
-        const int64_t total = num_weights * dim;
+        // counts / cursors [V], offsets [V + 1], list and sorted [n]
+        const size_t words = static_cast<size_t>(2 * num_weights + 1 + 2 * n);
+        Workspace ws(words * sizeof(int), index);
+        int* counts = static_cast<int*>(ws.get());
+        int* offsets = counts + num_weights;
+        int* list = offsets + num_weights + 1;
+        int* sorted = list + n;
+        zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(reinterpret_cast<uint32_t*>(counts),
+                                                                              num_weights);
+        if (n > 0) {
+            dispatch_index<float>(index_dtype, [&](auto tag) {
+                using I = decltype(tag);
+                embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(indices, n, num_weights,
+                                                                                   padding_idx, counts);
+            });
+        }
+        embedding_scan_kernel<<<1, kScanThreads, 0, st>>>(counts, offsets, num_weights);
+        if (n > 0) {
+            dispatch_index<float>(index_dtype, [&](auto tag) {
+                using I = decltype(tag);
+                embedding_fill_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
+                    indices, n, num_weights, padding_idx, offsets, counts, list);
+            });
+        }
         TP_AMD_DISPATCH_NN(dtype, T, {
-            // float32 accumulates in place; 16-bit types in a float32 buffer.
-            const bool in_place = std::is_same<T, float>::value;
-            Workspace acc_ws(in_place ? 0 : static_cast<size_t>(total) * sizeof(float), index);
-            float* acc = in_place ? static_cast<float*>(out) : static_cast<float*>(acc_ws.get());
-            zero_words_kernel<<<blocks_for(total, kBlock), kBlock, 0, st>>>(reinterpret_cast<uint32_t*>(acc),
-                                                                             total);
-            Workspace count_ws(scale_grad_by_freq ? static_cast<size_t>(num_weights) * sizeof(int) : 0, index);
-            int* counts = scale_grad_by_freq ? static_cast<int*>(count_ws.get()) : nullptr;
-            if (n > 0) {
-                dispatch_index<T>(index_dtype, [&](auto tag) {
-                    using I = decltype(tag);
-                    if (counts != nullptr) {
-                        zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(
-                            reinterpret_cast<uint32_t*>(counts), num_weights);
-                        embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
-                            indices, n, num_weights, padding_idx, counts);
-                    }
-                    embedding_backward_kernel<T, I><<<blocks_for(n, kBlock / kWave), kBlock, 0, st>>>(
-                        static_cast<const S_<T>*>(grad), indices, n, num_weights, dim, padding_idx, counts,
-                        acc);
-                });
-            }
-            if (!in_place) {
-                store_from_float_kernel<T><<<blocks_for(total, kBlock), kBlock, 0, st>>>(
-                    acc, static_cast<S_<T>*>(out), total);
+            const bool vec = dim % Packet<T>::N == 0 && aligned16(grad) && aligned16(out);
+            if (vec) {
+                embedding_gather_kernel<T, true><<<num_weights, kBlock, 0, st>>>(
+                    static_cast<const S_<T>*>(grad), offsets, list, sorted, static_cast<int>(n), dim,
+                    scale_grad_by_freq, static_cast<S_<T>*>(out));
+            } else {
+                embedding_gather_kernel<T, false><<<num_weights, kBlock, 0, st>>>(
+                    static_cast<const S_<T>*>(grad), offsets, list, sorted, static_cast<int>(n), dim,
+                    scale_grad_by_freq, static_cast<S_<T>*>(out));
             }
         });
         TP_AMD_HIP_CHECK(hipGetLastError());
@@ -907,6 +1373,18 @@ int tp_amd_launch_nll_loss_backward(int device, int dtype, int64_t n, int64_t cl
         DeviceGuard guard(index);
         const int64_t blocks = blocks_for(n * classes, kBlock);
         TP_AMD_DISPATCH_NN(dtype, T, {
+            constexpr int N = Packet<T>::N;
+            const int64_t per_row = blocks_for(classes / N, kBlock);
+            if (classes % N == 0 && aligned16(dx) && n * per_row <= 0x7fffffff) {
+                dispatch_index<T>(index_dtype, [&](auto tag) {
+                    using I = decltype(tag);
+                    nll_backward_rows_kernel<T, I><<<n * per_row, kBlock, 0, stream(index)>>>(
+                        static_cast<const S_<T>*>(grad), target, static_cast<const S_<T>*>(weight),
+                        static_cast<const S_<T>*>(total_weight), classes, static_cast<uint32_t>(per_row),
+                        ignore_index, reduction, static_cast<S_<T>*>(dx));
+                });
+                break;
+            }
             dispatch_index<T>(index_dtype, [&](auto tag) {
                 using I = decltype(tag);
                 nll_backward_kernel<T, I><<<blocks, kBlock, 0, stream(index)>>>(

@@ -42,9 +42,10 @@ LN_CASES = [
     ((300, 1024), (1024,)),      # packet rows, one wave
     ((64, 4096), (4096,)),       # several waves per row
     ((9, 1001), (1001,)),        # width not a whole number of packets
+    ((37, 12288), (12288,)),     # sixteen waves a row, the widest register layouts
     ((2, 40000), (40000,)),      # a row longer than the register-resident kernel holds
 ]
-LN_IDS = ["4x16", "3x5x24", "300x1024", "64x4096", "9x1001", "2x40000"]
+LN_IDS = ["4x16", "3x5x24", "300x1024", "64x4096", "9x1001", "37x12288", "2x40000"]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
@@ -192,6 +193,28 @@ def test_embedding_dense_backward(dev, ops, orc, dtype, pad, freq):
     assert_normwise(got, want, dtype, float(np.sqrt(counts.max())), "embedding backward")
     if pad >= 0:
         assert not orc.to_float(got[pad:pad + 1], dtype).any(), "padding row must stay zero"
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_embedding_dense_backward_heavy_rows(dev, ops, orc, dtype):
+    """A row taking more samples than the per-row LDS ordering holds (5000
+    of 6000 samples on row 7), ragged widths, int32 indices; two runs give
+    the same bits (each row sums its samples in sample order)."""
+    rng = np.random.default_rng(24)
+    V = 40
+    idx = rng.integers(0, V, size=6000).astype(np.int32)
+    idx[rng.permutation(6000)[:5000]] = 7
+    for D in (96, 5):
+        dy = sample(orc, (6000, D), dtype, 25)
+        g, i = dev.from_numpy(dy, dtype=dtype), dev.from_numpy(idx)
+        got = ops.embedding_dense_backward(g, i, V, -1, True).numpy()
+        again = ops.embedding_dense_backward(g, i, V, -1, True).numpy()
+        assert_bitexact(again, got, f"repeat D={D}")
+        want = orc.embedding_backward(dtype, dy, idx, V, -1, True)
+        assert_normwise(got, want, dtype, 1, f"heavy rows D={D}")
+        got = ops.embedding_dense_backward(g, i, V, -1, False).numpy()
+        want = orc.embedding_backward(dtype, dy, idx, V, -1, False)
+        assert_normwise(got, want, dtype, float(np.sqrt(5000)), f"heavy rows unscaled D={D}")
 
 
 def test_embedding_declines_sparse(dev, ops, orc):
