@@ -24,7 +24,7 @@ Also reported on the same line:
   sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,reduce}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,reduce,nn}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -401,7 +401,12 @@ def profile_launches(what: str, lib, ops, dev) -> None:
     gemm:    ten bf16 4096^3 products in each operand layout (A, B
              row-major; B transposed; A transposed; both transposed);
     reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
-             and bf16, five each."""
+             and bf16, five each;
+    nn:      the NN-layer suite's shapes, fp32 and bf16, five launches of
+             each operator: layer norm forward and backward [8192, 4096],
+             dropout p = 0.1 and its backward, embedding of 8192 indices into
+             [32000, 4096] and its dense gradient, nll_loss over
+             [8192, 32000] and its backward."""
     import ctypes as C
     if what == "traffic":
         a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
@@ -433,6 +438,31 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                 for dim in (-1, 0):
                     for _ in range(5):
                         fn(x, [dim])
+    elif what == "nn":
+        g = np.random.default_rng(0)
+        rows, D, V, C = 8192, 4096, 32000, 32000
+        idx = dev.from_numpy(g.integers(0, V, size=rows).astype(np.int64))
+        tgt = dev.from_numpy(g.integers(0, C, size=rows).astype(np.int64))
+        for dtype in (F32, BF16):
+            def put(shape):
+                d = dev.from_numpy(g.standard_normal(shape, dtype=np.float32))
+                return d if dtype == F32 else ops.to(d, dtype)
+            x, dy, w, b = put((rows, D)), put((rows, D)), put((D,)), put((D,))
+            _, mean, rstd = ops.native_layer_norm(x, (D,), w, b)
+            _, mask = ops.native_dropout(x, 0.1, True, 1)
+            table, logp = put((V, D)), put((rows, C))
+            _, total = ops.nll_loss(logp, tgt, None, 1)
+            one = ops.to(dev.from_numpy(np.array(1.0, np.float32)), dtype)
+            for _ in range(5):
+                ops.native_layer_norm(x, (D,), w, b)
+                ops.native_layer_norm_backward(dy, x, (D,), mean, rstd, w, b)
+                ops.native_dropout(x, 0.1, True, 7)
+                ops.native_dropout_backward(dy, mask, 1 / 0.9)
+                ops.embedding(table, idx)
+                ops.embedding_dense_backward(dy, idx, V)
+                ops.nll_loss(logp, tgt, None, 1)
+                ops.nll_loss_backward(one, logp, tgt, None, 1, -100, total)
+            del x, dy, w, b, mean, rstd, mask, table, logp, total
     else:
         raise SystemExit(f"unknown --profile {what}")
     assert lib.tp_amd_synchronize(0) == 0
@@ -446,7 +476,7 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "reduce"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "reduce", "nn"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
