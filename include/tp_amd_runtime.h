@@ -115,6 +115,55 @@ int tp_amd_event_record(void* event, int device);
 int tp_amd_event_elapsed_ms(void* start, void* stop, float* ms);
 int tp_amd_event_destroy(void* event);
 
+/* ---- profiler hooks (MLUProfiler.cpp:20-80, MLUActivity.cpp:87-258) ----- */
+
+/* Per-operation device time; replaces the notifier timer of
+ * MLUProfiler.cpp:20-51 (TensorPlay's prof::DeviceTimerHooks).  record
+ * places a pooled event on the device's stream; *marker is NULL when the
+ * device is out of range or the event cannot be placed (the hook then
+ * reports no time).  elapsed_ms waits for `end` and gives the milliseconds
+ * between two markers.  release returns a marker to the pool (NULL is
+ * ignored). */
+int tp_amd_timer_record(int device, void** marker);
+int tp_amd_timer_elapsed_ms(void* start, void* end, float* ms);
+void tp_amd_timer_release(void* marker);
+
+/* Copy directions of tp_amd_activity.copy_kind. */
+enum { TP_AMD_COPY_OTHER = 0, TP_AMD_COPY_HTOD = 1, TP_AMD_COPY_DTOH = 2, TP_AMD_COPY_DTOD = 3 };
+/* tp_amd_activity.external_id when the launching thread had none pushed. */
+#define TP_AMD_NO_EXTERNAL UINT64_MAX
+
+/* One kernel ('k') or copy ('m') the GPU ran during a tracing session,
+ * with the fields of TensorPlay's prof::GpuActivity that the reference's
+ * CNPAPI collector fills (MLUActivity.cpp:126-176, 233-247).  Times are on
+ * std::chrono::steady_clock, in nanoseconds. */
+typedef struct tp_amd_activity {
+    const char* name;       /* kernel symbol, or "Memcpy HtoD" / "DtoH" / "DtoD" */
+    char kind;              /* 'k' kernel, 'm' copy */
+    uint8_t copy_kind;      /* TP_AMD_COPY_* for copies */
+    uint64_t start_ns, end_ns;
+    uint64_t external_id;   /* the id pushed around the launch, or TP_AMD_NO_EXTERNAL */
+    uint32_t correlation;   /* the runtime's correlation id */
+    int32_t device;         /* GPU index (-1 unknown) */
+    int32_t stream;         /* queue index in order of first appearance (-1 for copies) */
+    uint64_t bytes;         /* bytes copied (copies) */
+} tp_amd_activity;
+
+/* Kernel-level tracing; replaces the CNPAPI collector of
+ * MLUActivity.cpp:87-258 (TensorPlay's prof::DeviceActivityHooks) with
+ * rocprofiler-sdk buffer tracing.  Available when the process starts with
+ * TP_AMD_DEVICE_TRACE=1 (the SDK takes a tool only before the HIP runtime
+ * starts; it is opened with dlopen); otherwise start fails and
+ * tp_amd_activity_error says why, and a session reports per-operation
+ * time only.  stop waits for the session's work, then hands out the
+ * records, valid until the next start.  push/pop bracket the launches of
+ * one operation with its id (a no-op while tracing is unavailable). */
+int tp_amd_activity_start(void);
+int tp_amd_activity_stop(const tp_amd_activity** records, size_t* count);
+int tp_amd_activity_push_external(uint64_t id);
+int tp_amd_activity_pop_external(void);
+const char* tp_amd_activity_error(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,27 @@ def scalar(value) -> Scalar:
     return Scalar(float(value), int(value) if abs(float(value)) < 2 ** 63 else 0, SCALAR_FLOAT, 0)
 
 
+COPY_OTHER, COPY_HTOD, COPY_DTOH, COPY_DTOD = 0, 1, 2, 3
+NO_EXTERNAL = 2 ** 64 - 1
+
+
+class Activity(C.Structure):
+    """tp_amd_activity: one kernel or copy of a tracing session."""
+
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("kind", C.c_char),
+        ("copy_kind", C.c_uint8),
+        ("start_ns", C.c_uint64),
+        ("end_ns", C.c_uint64),
+        ("external_id", C.c_uint64),
+        ("correlation", C.c_uint32),
+        ("device", C.c_int32),
+        ("stream", C.c_int32),
+        ("bytes", C.c_uint64),
+    ]
+
+
 T = C.POINTER(Tensor)
 I64P = C.POINTER(C.c_int64)
 VP = C.c_void_p
@@ -90,6 +111,14 @@ PROTOTYPES = {
     "tp_amd_event_record": (i32, [VP, i32]),
     "tp_amd_event_elapsed_ms": (i32, [VP, VP, C.POINTER(C.c_float)]),
     "tp_amd_event_destroy": (i32, [VP]),
+    "tp_amd_timer_record": (i32, [i32, C.POINTER(VP)]),
+    "tp_amd_timer_elapsed_ms": (i32, [VP, VP, C.POINTER(C.c_float)]),
+    "tp_amd_timer_release": (None, [VP]),
+    "tp_amd_activity_start": (i32, []),
+    "tp_amd_activity_stop": (i32, [C.POINTER(C.POINTER(Activity)), C.POINTER(C.c_size_t)]),
+    "tp_amd_activity_push_external": (i32, [u64]),
+    "tp_amd_activity_pop_external": (i32, []),
+    "tp_amd_activity_error": (C.c_char_p, []),
     # kernels (tp_amd_kernels.h)
     "tp_amd_launch_binary": (i32, [i32, i32, i32, i32, I64P, VP, I64P, VP, I64P, VP, I64P, f32]),
     "tp_amd_launch_affine": (i32, [i32, i32, i64, VP, f32, f32, VP]),

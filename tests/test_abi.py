@@ -93,7 +93,7 @@ def test_tensorplay_adapter_compiles():
     if gxx is None:
         import pytest
         pytest.skip("g++ not available")
-    for source in ("Kernels.cpp", "Backend.cpp"):
+    for source in ("Kernels.cpp", "Backend.cpp", "Profiler.cpp"):
         cmd = [gxx, "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
                "-I", os.path.join(ROOT, "tests", "native", "tensorplay_api"),
                "-I", os.path.join(ROOT, "include"), os.path.join(ADAPTER, source)]

@@ -6,6 +6,7 @@ sizes, and the decline paths that send an operator to the host
 BlasKernels.cpp:244-248) -- each checked against hand-derived results."""
 
 import ctypes as C
+import os
 import importlib
 
 import numpy as np
@@ -113,3 +114,22 @@ def test_null_arguments_are_errors(lib):
     assert lib.tp_amd_add(None, None, abi.scalar(1), C.byref(out)) == -1
     assert b"null tensor" in lib.tp_mlu_last_error()
     assert lib.tp_amd_exp(None, C.byref(out)) == -1
+
+
+def test_profiler_without_a_device_or_tracing(amd):
+    """Without a GPU a timer places no marker and reports no time, and
+    kernel-level tracing (off unless the process starts with
+    TP_AMD_DEVICE_TRACE=1) refuses to start with the reason."""
+    if os.environ.get("TP_AMD_DEVICE_TRACE") == "1":
+        pytest.skip("tracing requested for this process")
+    prof = importlib.import_module("tensorplay-mlu_amd.profiler")
+    runtime = importlib.import_module("tensorplay-mlu_amd.runtime")
+    if runtime.device_count() == 0:
+        t = prof.Timer(0)
+        t.start()
+        t.stop()
+        assert t.elapsed_ms() is None
+    assert not prof.Trace.available()
+    assert "TP_AMD_DEVICE_TRACE" in prof.Trace.unavailable_reason()
+    with pytest.raises(RuntimeError, match="TP_AMD_DEVICE_TRACE"):
+        prof.Trace().start()
