@@ -243,4 +243,54 @@ __device__ __forceinline__ float wave_allreduce(float v, Op op) {
     return op(op(a, b), op(c, d));
 }
 
+// ---- buffer access ------------------------------------------------------------
+//
+// Row kernels address rows through buffer resources: a 16-byte access past
+// the resource's range is dropped by the hardware (a load gives zeros), so a
+// thread issues its loads and stores without a branch around each, and the
+// compiler can count the outstanding ones exactly -- it waits for a
+// prefetched row without also waiting for the stores issued after it.
+
+using Rsrc = __amdgpu_buffer_rsrc_t;
+typedef unsigned int U32x4 __attribute__((ext_vector_type(4)));
+constexpr int kNt = 2;  // cache policy: non-temporal
+
+// A resource over `bytes` bytes at `base`; 0 bytes makes every access out of
+// range (nothing is read or written).
+__device__ __forceinline__ Rsrc buffer_over(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(Rsrc r, uint32_t offset) {
+    const U32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kNt);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void buffer_store16(Rsrc r, uint32_t offset, const uint4& v) {
+    const U32x4 d = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(d, r, offset, 0, kNt);
+}
+
+__device__ __forceinline__ float buffer_load_f32(Rsrc r, uint32_t offset) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+}
+
+__device__ __forceinline__ void buffer_store_f32(Rsrc r, uint32_t offset, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, offset, 0, 0);
+}
+
+// A wave-uniform 64-bit value in scalar registers.
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+constexpr uint32_t kOutOfRange = 0xfffffff0u;  // an offset past any resource used here
+
+// Waits for every outstanding memory operation.  Before a software-pipelined
+// row loop this leaves nothing pending on entry, so the waits the compiler
+// places at the loop head follow the loop's own issue order alone.
+__device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
+
 }  // namespace tp_amd

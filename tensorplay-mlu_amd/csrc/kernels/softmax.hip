@@ -138,26 +138,24 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_rows_kernel(
 // block per row would leave the CU idle while each row's loads are in
 // flight.  Instead a grid of one block per CU walks the rows, and the loads
 // of its next row are issued before the current row is reduced and written
-// (two register sets, alternating).
+// (two register sets, alternating).  Rows are addressed through buffer
+// resources (a row and the whole grid under 4 GiB of offsets per row): no
+// branch surrounds a load or store, so the compiler waits for a prefetched
+// row without also waiting for the stores issued after it.
 template <typename T, int VPT>
 struct RowBuffer {
     uint4 raw[VPT];
 };
 
+// Row `row` (zeros past the last row or the row's end).
 template <typename T, int VPT>
-__device__ __forceinline__ void fetch_row(RowBuffer<T, VPT>& b,
-                                          const typename Elem<T>::storage* xr, int64_t npk,
-                                          int tid) {
-    constexpr int N = Packet<T>::N;
-    // -inf in the storage format pads the packets past the row's end.
-    constexpr uint32_t kNegInf = sizeof(typename Elem<T>::storage) == 4 ? 0xff800000u
-                                 : std::is_same_v<T, bf16_t>           ? 0xff80ff80u
-                                                                       : 0xfc00fc00u;
+__device__ __forceinline__ void fetch_row(RowBuffer<T, VPT>& b, const typename Elem<T>::storage* x,
+                                          int64_t row, int64_t rows, int64_t D, int tid) {
+    const bool ok = row < rows;
+    const Rsrc r = buffer_over(x + (ok ? row : 0) * D,
+                               ok ? static_cast<uint32_t>(D * sizeof(typename Elem<T>::storage)) : 0u);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
-        b.raw[k] = q < npk ? load_raw_nt(xr + q * N) : make_uint4(kNegInf, kNegInf, kNegInf, kNegInf);
-    }
+    for (int k = 0; k < VPT; ++k) b.raw[k] = buffer_load16(r, static_cast<uint32_t>(tid + k * 16 * kWave) * 16u);
 }
 
 __device__ __forceinline__ uint32_t& word(uint4& v, int i) {
@@ -171,36 +169,38 @@ __device__ __forceinline__ void finish_row_f32(RowBuffer<float, VPT>& b, float* 
                                                int tid, bool log, float* scratch) {
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < VPT; ++k)
+    for (int k = 0; k < VPT; ++k) {
+        const bool in = tid + k * 16 * kWave < npk;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) m = fmaxf(m, __uint_as_float(word(b.raw[k], j)));
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, in ? __uint_as_float(word(b.raw[k], j)) : -INFINITY);
+    }
     m = row_reduce<16, true>(m, scratch);
     const float shift = m == -INFINITY ? 0.0f : m;
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < VPT; ++k)
+    for (int k = 0; k < VPT; ++k) {
+        const bool in = tid + k * 16 * kWave < npk;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float d = __uint_as_float(word(b.raw[k], j)) - shift;
             const float e = exp_fast(d);
-            s += e;
+            s += in ? e : 0.0f;
             word(b.raw[k], j) = __float_as_uint(log ? d : e);
         }
+    }
     s = row_reduce<16, false>(s, scratch);
     const float lse = logf(s);
     const float inv = 1.0f / s;
+    const Rsrc out = buffer_over(yr, static_cast<uint32_t>(npk * 16));
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
-        if (q < npk) {
-            uint4 o = b.raw[k];
+        uint4 o = b.raw[k];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float v = __uint_as_float(word(o, j));
-                word(o, j) = __float_as_uint(log ? v - lse : v * inv);
-            }
-            store_raw_nt(yr + q * 4, o);
+        for (int j = 0; j < 4; ++j) {
+            const float v = __uint_as_float(word(o, j));
+            word(o, j) = __float_as_uint(log ? v - lse : v * inv);
         }
+        buffer_store16(out, static_cast<uint32_t>(tid + k * 16 * kWave) * 16u, o);
     }
 }
 
@@ -217,9 +217,13 @@ __device__ __forceinline__ void finish_row(RowBuffer<T, VPT>& b,
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
+        const bool in = tid + k * 16 * kWave < npk;
         unpack<T>(b.raw[k], v[k]);
 #pragma unroll
-        for (int j = 0; j < N; ++j) m = fmaxf(m, v[k][j]);
+        for (int j = 0; j < N; ++j) {
+            v[k][j] = in ? v[k][j] : -INFINITY;
+            m = fmaxf(m, v[k][j]);
+        }
     }
     m = row_reduce<16, true>(m, scratch);
     const float shift = m == -INFINITY ? 0.0f : m;
@@ -236,15 +240,13 @@ __device__ __forceinline__ void finish_row(RowBuffer<T, VPT>& b,
     s = row_reduce<16, false>(s, scratch);
     const float lse = logf(s);
     const float inv = 1.0f / s;
+    const Rsrc out = buffer_over(yr, static_cast<uint32_t>(npk * 16));
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-        const int64_t q = tid + static_cast<int64_t>(k) * 16 * kWave;
-        if (q < npk) {
-            float o[N];
+        float o[N];
 #pragma unroll
-            for (int j = 0; j < N; ++j) o[j] = log ? v[k][j] - lse : v[k][j] * inv;
-            store_raw_nt(yr + q * N, pack<T>(o));
-        }
+        for (int j = 0; j < N; ++j) o[j] = log ? v[k][j] - lse : v[k][j] * inv;
+        buffer_store16(out, static_cast<uint32_t>(tid + k * 16 * kWave) * 16u, pack<T>(o));
     }
 }
 
@@ -259,16 +261,15 @@ __global__ __launch_bounds__(16 * kWave) void softmax_rows_stream_kernel(
     const int64_t step = gridDim.x;
     RowBuffer<T, VPT> a, b;
     int64_t row = blockIdx.x;
-    if (row < rows) fetch_row<T, VPT>(a, x + row * D, npk, tid);
+    fetch_row<T, VPT>(a, x, row, rows, D, tid);
+    drain();
     // Uniform per block: every thread walks the same rows.
-    while (row < rows) {
-        if (row + step < rows) fetch_row<T, VPT>(b, x + (row + step) * D, npk, tid);
+    for (; row < rows; row += 2 * step) {
+        fetch_row<T, VPT>(b, x, row + step, rows, D, tid);
         finish_row<T, VPT>(a, y + row * D, npk, tid, log, scratch);
-        row += step;
-        if (row >= rows) break;
-        if (row + step < rows) fetch_row<T, VPT>(a, x + (row + step) * D, npk, tid);
-        finish_row<T, VPT>(b, y + row * D, npk, tid, log, scratch);
-        row += step;
+        if (row + step >= rows) break;
+        fetch_row<T, VPT>(a, x, row + 2 * step, rows, D, tid);
+        finish_row<T, VPT>(b, y + (row + step) * D, npk, tid, log, scratch);
     }
 }
 
@@ -324,6 +325,72 @@ __global__ __launch_bounds__(block_threads<WAVES>()) void softmax_backward_rows_
             }
             store_raw_nt(dx + base + q * N, pack<T>(o));
         }
+    }
+}
+
+// The backward of rows that need a whole 16-wave block, the forward's
+// stream scheme for two inputs: one block per CU walks the rows with the
+// next row's y and dy loaded before this row's reduction (two register sets
+// of raw packets), all through buffer resources.  Packets past the row's
+// end load as zeros and add nothing to the row sum.
+template <typename T, int VPT>
+struct GradRows {
+    uint4 y[VPT], g[VPT];
+};
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(16 * kWave) void softmax_backward_stream_kernel(
+    const typename Elem<T>::storage* y, const typename Elem<T>::storage* dy,
+    typename Elem<T>::storage* dx, int64_t rows, int64_t D, bool log) {
+    constexpr int N = Packet<T>::N;
+    __shared__ float scratch[16];
+    const int tid = threadIdx.x;
+    const uint32_t row_bytes = static_cast<uint32_t>(D * sizeof(typename Elem<T>::storage));
+    const int64_t step = gridDim.x;
+    auto fetch = [&](GradRows<T, VPT>& b, int64_t row) {
+        const bool ok = row < rows;
+        const int64_t at = (ok ? row : 0) * D;
+        const Rsrc ry = buffer_over(y + at, ok ? row_bytes : 0u);
+        const Rsrc rg = buffer_over(dy + at, ok ? row_bytes : 0u);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const uint32_t off = static_cast<uint32_t>(tid + k * 16 * kWave) * 16u;
+            b.y[k] = buffer_load16(ry, off);
+            b.g[k] = buffer_load16(rg, off);
+        }
+    };
+    auto finish = [&](const GradRows<T, VPT>& b, int64_t row) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            float a[N], g[N];
+            unpack<T>(b.y[k], a);
+            unpack<T>(b.g[k], g);
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += log ? g[j] : g[j] * a[j];
+        }
+        s = row_reduce<16, false>(s, scratch);
+        const Rsrc out = buffer_over(dx + row * D, row_bytes);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            float a[N], g[N], o[N];
+            unpack<T>(b.y[k], a);
+            unpack<T>(b.g[k], g);
+#pragma unroll
+            for (int j = 0; j < N; ++j) o[j] = log ? g[j] - exp_fast(a[j]) * s : a[j] * (g[j] - s);
+            buffer_store16(out, static_cast<uint32_t>(tid + k * 16 * kWave) * 16u, pack<T>(o));
+        }
+    };
+    GradRows<T, VPT> a, b;
+    int64_t row = blockIdx.x;
+    fetch(a, row);
+    drain();
+    for (; row < rows; row += 2 * step) {
+        fetch(b, row + step);
+        finish(a, row);
+        if (row + step >= rows) break;
+        fetch(a, row + 2 * step);
+        finish(b, row + step);
     }
 }
 
@@ -678,7 +745,17 @@ void softmax_backward_typed(int device, bool log, int64_t outer, int64_t D, int6
     if (inner == 1) {
         const bool vec = D % N == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
         const RowConfig c = choose_config<T>(D);
-        if (vec && c.waves > 0) {
+        if (vec && c.waves == 16 && c.ept / N <= 4) {
+            // Rows that need a whole block: one block per CU walks them.
+            const int64_t grid = outer < cu_count(device) ? outer : cu_count(device);
+            if (c.ept / N <= 2) {
+                softmax_backward_stream_kernel<T, 2><<<grid, 16 * kWave, 0, st>>>(
+                    static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), outer, D, log);
+            } else {
+                softmax_backward_stream_kernel<T, 4><<<grid, 16 * kWave, 0, st>>>(
+                    static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), outer, D, log);
+            }
+        } else if (vec && c.waves > 0) {
             launch_backward_config<T>(c, device, y, dy, dx, outer, D, log);
         } else if (vec) {
             softmax_backward_rows_long_kernel<T, 2><<<outer, kBlock, 0, st>>>(
