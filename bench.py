@@ -24,7 +24,7 @@ Also reported on the same line:
   sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,reduce,nn}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,reduce,softmax,nn}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -402,6 +402,8 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              row-major; B transposed; A transposed; both transposed);
     reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
              and bf16, five each;
+    softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
+             X2 [4096, 32000], fp32 and bf16, five each;
     nn:      the NN-layer suite's shapes, fp32 and bf16, five launches of
              each operator: layer norm forward and backward [8192, 4096],
              dropout p = 0.1 and its backward, embedding of 8192 indices into
@@ -438,6 +440,19 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                 for dim in (-1, 0):
                     for _ in range(5):
                         fn(x, [dim])
+    elif what == "softmax":
+        g = np.random.default_rng(0)
+        for shape in ((32768, 4096), (4096, 32000)):
+            x32 = dev.from_numpy(g.standard_normal(shape, dtype=np.float32) * np.float32(2.0))
+            g32 = dev.from_numpy(g.standard_normal(shape, dtype=np.float32))
+            for dtype in (F32, BF16):
+                x, dy = (x32, g32) if dtype == F32 else (ops.to(x32, dtype), ops.to(g32, dtype))
+                y = ops.softmax(x, -1)
+                for _ in range(5):
+                    ops.softmax(x, -1)
+                    ops._softmax_backward_data(dy, y, -1, dtype)
+                del x, dy, y
+            del x32, g32
     elif what == "nn":
         g = np.random.default_rng(0)
         rows, D, V, C = 8192, 4096, 32000, 32000
@@ -476,7 +491,7 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "reduce", "nn"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "reduce", "softmax", "nn"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
