@@ -371,17 +371,20 @@ namespace big {
 //
 // Operand tiles move from memory straight into LDS with buffer loads (16
 // bytes a lane, no registers in between).  Each operand tile is 32 KB in one
-// of two layouts:
+// of two layouts, swizzled for gfx950's LDS of 64 four-byte banks (256 bytes
+// a clock: 16 lanes of a ds_read_b128, 32 lanes of an 8-byte read):
 //   * K-major operand: 256 rows (M or N) of 128 bytes, one row = the tile's
-//     64 k; logical 16-byte chunk c of row r sits at slot c ^ (r & 7).  A
+//     64 k; logical 16-byte chunk c of row r sits at slot c ^ kswz(r).  A
 //     load instruction fills 8 rows; a fragment read (ds_read_b128: 32 rows,
-//     one chunk) then touches every bank once per 8 lanes.
+//     one chunk) puts each 16-lane group's 16 rows on 64 distinct banks.
 //   * M/N-major operand (a transposed view, read in place): 64 rows (k) of
-//     512 bytes, chunk c of row k at slot c ^ 2 (k & 3).  A load instruction
+//     512 bytes, chunk c of row k at slot c ^ nswz(k).  A load instruction
 //     fills 2 rows.  Fragments come from ds_read_b64_tr_b16, which hands
 //     each lane of a 16-lane group one column of a 4 x 16 block: two of them
-//     give a lane its 8 consecutive k; the four rows a group reads fall in
-//     distinct banks.
+//     give a lane its 8 consecutive k; the 4 rows x 64 bytes that 32 lanes
+//     read fall on 64 distinct banks.
+// Both swizzles also keep 8 lanes of a b128 read (16 of a b64 read) on 32
+// distinct banks.
 // The loads for K tile kt + 1 go out during the first half of step kt into
 // the other LDS stage, spread between the MFMAs.
 constexpr int BM = 256, BN = 256, BK = 64;
@@ -389,6 +392,14 @@ constexpr int TILE = 256 * 128;   // bytes per operand tile
 constexpr int STAGE = 2 * TILE;   // bytes per LDS stage
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// K-major: rows r and r + 8 (one 16-lane group) differ in the low bit of the
+// slot; rows of one parity (the same half of a 256-byte bank line) take 8
+// distinct slots.
+__device__ __forceinline__ int kswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// M/N-major: rows k..k+3 move a 4-chunk span (64 bytes) to four distinct
+// quarters of a bank line, and a 2-chunk span to four distinct slots mod 8.
+__device__ __forceinline__ int nswz(int k) { return (2 * (k & 3)) ^ (8 * (k & 1)); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
@@ -411,19 +422,19 @@ struct Operand {
             // element (r, k) at X[r * ld + k]; a load's lane L fills slot L % 8
             // of row L / 8 of its 8-row group
             res = rsrc(static_cast<const uint16_t*>(X) + mn0 * ld, static_cast<uint32_t>(256 * ld * 2));
-            const int row = lane >> 3, chunk = (lane & 7) ^ row;
+            const int row = lane >> 3, chunk = (lane & 7) ^ kswz(8 * wave + row);
             voff = static_cast<uint32_t>((row * ld + chunk * 8) * 2);
             sbase = static_cast<uint32_t>(wave * 8 * ld * 2);
             sstep = static_cast<uint32_t>(W * 8 * ld * 2);
             kstep = BK * 2;
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                frag[s] = (wbase + l32) * 128 + ((((2 * s + half) ^ (l32 & 7))) << 4);
+                frag[s] = (wbase + l32) * 128 + (((2 * s + half) ^ kswz(l32)) << 4);
         } else {
             // element (k, r) at X[k * ld + r]; a load fills 2 rows of k
             res = rsrc(static_cast<const uint16_t*>(X) + mn0, static_cast<uint32_t>(K * ld * 2));
             const int row = lane >> 5;
-            const int chunk = (lane & 31) ^ (2 * ((2 * (wave & 1) + row) & 3));
+            const int chunk = (lane & 31) ^ nswz(2 * (wave & 1) + row);
             voff = static_cast<uint32_t>((row * ld + chunk * 8) * 2);
             sbase = static_cast<uint32_t>(2 * wave * ld * 2);
             sstep = static_cast<uint32_t>(2 * W * ld * 2);
@@ -436,7 +447,7 @@ struct Operand {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const int col = wbase + t * 32 + 16 * (g & 1) + 4 * (pl % 4);
-                frag[t] = krow * 512 + (((col / 8) ^ (2 * (krow & 3))) << 4) + (col % 8) * 2;
+                frag[t] = krow * 512 + (((col / 8) ^ nswz(krow)) << 4) + (col % 8) * 2;
             }
         }
     }
