@@ -99,12 +99,23 @@ __device__ __forceinline__ uint32_t component(const uint4& v, int i) {
 
 // One operand's tile loader: R rows (M or N) x BK, into LDS [R][BK + pad].
 // KMAJOR: element (r, k) at X[r * ld + k]; otherwise at X[k * ld + r].
+// A float32 operand with its M (or N) axis contiguous (KROWS) is copied as it
+// lies instead, [BK][R + 8]: 16-byte loads along the row, 32 lanes a row, and
+// 16-byte LDS stores; the fragment reads then take a lane's 4 consecutive k
+// as 4 single-float reads, the two lane halves 4 rows apart, which the pad of
+// 8 floats puts on the other half of the 64 banks.  (Transposing 4 x 4
+// blocks in registers before a K-major store, as the 16-bit types do, left
+// the float32 NN and TN products waiting 7-10x longer than NT: 4096^3 NN
+// 1469 us, TN 1606 us, NT 1261 us.)
 template <typename T, int R, bool KMAJOR, int THREADS>
 struct TileLoader {
     using S = typename Elem<T>::storage;
     static constexpr int V = Mfma<T>::V;
     static constexpr int BK = Mfma<T>::BK;
     static constexpr int LDS_STRIDE = BK + 16 / sizeof(S);  // elements per LDS row
+    static constexpr bool KROWS = !KMAJOR && sizeof(S) == 4;
+    static constexpr int KR_STRIDE = R + 8;                  // KROWS: elements per LDS row (one k)
+    static_assert(!KROWS || BK * KR_STRIDE <= R * LDS_STRIDE, "KROWS tile fits the K-major space");
     // K-major: R * BK / V vectors; MN-major: (R / V) * (BK / 4) units of 4
     // vectors (V along M/N by 4 along K).
     static constexpr int kLoads = (KMAJOR ? R * BK / V : (R / V) * (BK / 4) * 4) / THREADS;
@@ -117,7 +128,19 @@ struct TileLoader {
     __device__ __forceinline__ void load(const S* X, int64_t ld, int64_t r0, int64_t rows,
                                          int64_t k0, int64_t K) {
         const int tid = threadIdx.x;
-        if constexpr (KMAJOR) {
+        if constexpr (KROWS) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int v = tid + i * THREADS;
+                const int k = v / (R / V), c = v % (R / V);
+                const int64_t gr = r0 + c * V, gk = k0 + k;
+                if (gr < rows && gk < K) {
+                    reg[i] = *reinterpret_cast<const uint4*>(X + gk * ld + gr);
+                } else {
+                    reg[i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        } else if constexpr (KMAJOR) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) {
                 const int v = tid + i * THREADS;
@@ -150,7 +173,14 @@ struct TileLoader {
 
     __device__ __forceinline__ void store(S* lds) const {
         const int tid = threadIdx.x;
-        if constexpr (KMAJOR) {
+        if constexpr (KROWS) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int v = tid + i * THREADS;
+                const int k = v / (R / V), c = v % (R / V);
+                *reinterpret_cast<uint4*>(lds + k * KR_STRIDE + c * V) = reg[i];
+            }
+        } else if constexpr (KMAJOR) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) {
                 const int v = tid + i * THREADS;
@@ -269,19 +299,31 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
             // their latency hides behind the matrix work.
             constexpr int NSUB = BK / KSUB;
             uint4 af[2][TM], bf[2][TN];
+            // A lane's 4 consecutive k (k0 + j for component j) of row or
+            // column `rc`, from either LDS layout.
+            auto frag = [&](const S* base, int rc, int k0, auto krows) -> uint4 {
+                if constexpr (decltype(krows)::value) {
+                    constexpr int KS = LA::KR_STRIDE;
+                    static_assert(KS == LB::KR_STRIDE, "float32 tiles of one width");
+                    const S* q = base + k0 * KS + rc;
+                    uint4 v;
+                    __builtin_memcpy(&v.x, q, 4);
+                    __builtin_memcpy(&v.y, q + KS, 4);
+                    __builtin_memcpy(&v.z, q + 2 * KS, 4);
+                    __builtin_memcpy(&v.w, q + 3 * KS, 4);
+                    return v;
+                } else {
+                    return *reinterpret_cast<const uint4*>(base + rc * LDS_STRIDE + k0);
+                }
+            };
             auto fetch = [&](int s, int buf) {
+                const int k0 = s * KSUB + half * (KSUB / 2);
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int row = wm * kWaveM + i * 32 + l32;
-                    af[buf][i] = *reinterpret_cast<const uint4*>(As + row * LDS_STRIDE + s * KSUB +
-                                                                 half * (KSUB / 2));
-                }
+                for (int i = 0; i < TM; ++i)
+                    af[buf][i] = frag(As, wm * kWaveM + i * 32 + l32, k0, std::integral_constant<bool, LA::KROWS>{});
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int col = wn * kWaveN + j * 32 + l32;
-                    bf[buf][j] = *reinterpret_cast<const uint4*>(Bs + col * LDS_STRIDE + s * KSUB +
-                                                                 half * (KSUB / 2));
-                }
+                for (int j = 0; j < TN; ++j)
+                    bf[buf][j] = frag(Bs, wn * kWaveN + j * 32 + l32, k0, std::integral_constant<bool, LB::KROWS>{});
             };
             fetch(0, 0);
 #pragma unroll
