@@ -24,7 +24,7 @@ Also reported on the same line:
   sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,reduce,softmax,nn}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,gemm32,reduce,softmax,nn}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -400,6 +400,7 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              FETCH_SIZE / WRITE_SIZE counters, then ten of the dominant kernel;
     gemm:    ten bf16 4096^3 products in each operand layout (A, B
              row-major; B transposed; A transposed; both transposed);
+    gemm32:  the same in float32, five products a layout;
     reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
              and bf16, five each;
     softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
@@ -421,15 +422,18 @@ def profile_launches(what: str, lib, ops, dev) -> None:
         for _ in range(10):
             assert lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, a.data_ptr, sa, row.data_ptr, sb,
                                             out.data_ptr, sa, 1.0) == 0
-    elif what == "gemm":
+    elif what in ("gemm", "gemm32"):
         K = 4096
+        dt, reps = (BF16, 10) if what == "gemm" else (F32, 5)
         g = np.random.default_rng(0)
-        a = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
-        b = ops.to(dev.from_numpy(g.standard_normal((K, K), dtype=np.float32)), BF16)
-        c = ops.empty((K, K), BF16)
+        a = dev.from_numpy(g.standard_normal((K, K), dtype=np.float32))
+        b = dev.from_numpy(g.standard_normal((K, K), dtype=np.float32))
+        if dt != F32:
+            a, b = ops.to(a, dt), ops.to(b, dt)
+        c = ops.empty((K, K), dt)
         for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
-            for _ in range(10):
-                assert lib.tp_amd_launch_gemm(0, BF16, 1, K, K, K, 1.0, a.data_ptr, K, 0, ta,
+            for _ in range(reps):
+                assert lib.tp_amd_launch_gemm(0, dt, 1, K, K, K, 1.0, a.data_ptr, K, 0, ta,
                                               b.data_ptr, K, 0, tb, 0.0, None, 0, 0, 0,
                                               c.data_ptr, K, 0) == 0
     elif what == "reduce":
@@ -491,7 +495,7 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "reduce", "softmax", "nn"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "softmax", "nn"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
