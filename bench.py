@@ -21,7 +21,10 @@ Also reported on the same line:
   from HIP events;
 * ``cpu_baseline``: the repository's C oracle (a CPU port of the same
   operators, float64 arithmetic, OpenMP) timed on this host on a bounded
-  sample of the same workload.
+  sample of the same workload;
+* ``suite_cpu``: the same oracle on bounded samples of the suite's other
+  sections (config 3, config 4, config 5b, layer norm), each in its
+  section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
   python bench.py --profile {traffic,gemm,gemm32,reduce,softmax,nn}   # launch sequences for rocprofv3
@@ -391,6 +394,133 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 8):
                       "OpenMP; TensorPlay's CPU path is not installed)"}
 
 
+def cpu_suite(seconds_each: float = 3.0) -> dict:
+    """CPU figures beside the suite's sections, in each section's unit: the C
+    oracle (float64 arithmetic, OpenMP over the host's cores) on a bounded
+    sample of the section's workload, repeated until ``seconds_each`` have
+    passed (at least once).  Operand preparation is not timed."""
+    from oracle import binding as orc
+
+    cores = int(orc.lib().orc_num_threads())
+    note = "repository C oracle, float64 arithmetic, OpenMP; TensorPlay's CPU path is not installed"
+    g = np.random.default_rng(0)
+
+    def timed(fn):
+        work, passes, t0 = 0, 0, time.perf_counter()
+        while passes == 0 or time.perf_counter() - t0 < seconds_each:
+            work += fn()
+            passes += 1
+        return work, time.perf_counter() - t0, passes
+
+    def entry(value, unit, secs, passes, sample):
+        return {"value": float(f"{value:.4g}"), "unit": unit, "cores": cores, "kind": "port",
+                "seconds": round(secs, 2), "sample": f"{sample}, {passes} pass(es) ({note})"}
+
+    out = {}
+    # Config 3: 1024 of X1's 32768 rows, fp32 and bf16.
+    rows, D = 1024, 4096
+    x32 = g.standard_normal((rows, D), dtype=np.float32) * np.float32(2.0)
+    g32 = g.standard_normal((rows, D), dtype=np.float32)
+    prep = {}
+    for dt in (F32, BF16):
+        X, G = orc.from_float(x32, dt), orc.from_float(g32, dt)
+        prep[dt] = (X, G, orc.softmax(False, dt, X, rows, D, 1), orc.softmax(True, dt, X, rows, D, 1))
+
+    def config3():
+        total = 0
+        for dt, (X, G, Y, LY) in prep.items():
+            n = rows * D * ESIZE[dt]
+            for op in (0, 1, 2, 3):  # sum, mean, amax, amin over dim -1, then dim 0
+                orc.reduce(op, dt, X, rows, D, 1)
+                orc.reduce(op, dt, X, 1, rows, D)
+                total += 2 * n + (rows + D) * ESIZE[dt]
+            for log in (False, True):
+                orc.softmax(log, dt, X, rows, D, 1)
+                orc.softmax_backward(log, dt, LY if log else Y, G, rows, D, 1)
+                total += 5 * n
+        return total
+
+    work, secs, passes = timed(config3)
+    out["config3"] = entry(work / secs / 1e9, "GB/s", secs, passes,
+                           "sum/mean/amax/amin over dim -1 and 0, softmax and log_softmax forward "
+                           f"and backward on {rows} of X1's 32768 rows [x 4096], fp32 and bf16")
+    del prep
+    # Config 4: 64 rows of the 4096^3 products, fp32 and bf16 (fp32 accumulation).
+    m, K = 64, 4096
+    ops4 = {}
+    for dt in (F32, BF16):
+        a = orc.from_float(g.standard_normal((m, K), dtype=np.float32) * np.float32(K ** -0.25), dt)
+        b = orc.from_float(g.standard_normal((K, K), dtype=np.float32) * np.float32(K ** -0.25), dt)
+        ops4[dt] = (a, b)
+
+    def config4():
+        for dt, (a, b) in ops4.items():
+            orc.gemm(dt, a, b)
+        return 2 * (2 * m * K * K)
+
+    work, secs, passes = timed(config4)
+    out["config4"] = entry(work / secs / 1e12, "TFLOP/s", secs, passes,
+                           f"mm {m}x{K}x{K} ({m} of the 4096 rows of config 4's mm), fp32 and bf16")
+    del ops4
+    # Config 5b: the MLP training step on 32 of the batch's 8192 rows (four
+    # Linear(4096, 4096) + ReLU, Linear(4096, 1000), log_softmax, NLL through
+    # mul + sum with a one-hot, backward, SGD), every operator from the oracle.
+    bsz, width, classes, lr = 32, 4096, 1000, 1e-3
+    Ws = [g.standard_normal((width, width), dtype=np.float32) * np.float32(width ** -0.5) for _ in range(4)]
+    Ws.append(g.standard_normal((classes, width), dtype=np.float32) * np.float32(width ** -0.5))
+    bs = [np.zeros(w.shape[0], np.float32) for w in Ws]
+    x = g.standard_normal((bsz, width), dtype=np.float32)
+    onehot = np.zeros((bsz, classes), np.float32)
+    onehot[np.arange(bsz), g.integers(0, classes, size=bsz)] = 1.0
+    per_row = 2 * (4 * width * width + width * classes) * 2 + 2 * (3 * width * width + width * classes)
+
+    def config5b():
+        hs, zs = [x], []
+        for li in range(4):
+            zs.append(orc.gemm(F32, hs[-1], Ws[li], trans_b=True, beta=1.0, cin=bs[li]))
+            hs.append(orc.unary(8, F32, zs[-1]))
+        logits = orc.gemm(F32, hs[-1], Ws[4], trans_b=True, beta=1.0, cin=bs[4])
+        lp = orc.softmax(True, F32, logits, bsz, classes, 1)
+        orc.reduce(0, F32, orc.binary(1, F32, lp, onehot), 1, bsz * classes, 1)
+        dlogits = orc.softmax_backward(True, F32, lp, orc.affine(F32, onehot, -1.0 / bsz, 0.0),
+                                       bsz, classes, 1)
+        grads = [None] * 5
+        grads[4] = (orc.gemm(F32, dlogits, hs[4], trans_a=True), orc.reduce(0, F32, dlogits, 1, bsz, classes))
+        da = orc.gemm(F32, dlogits, Ws[4])
+        for li in range(3, -1, -1):
+            dz = orc.activation_backward(0, F32, da, zs[li], 0.0)
+            grads[li] = (orc.gemm(F32, dz, hs[li], trans_a=True), orc.reduce(0, F32, dz, 1, bsz, width))
+            if li > 0:
+                da = orc.gemm(F32, dz, Ws[li])
+        for li in range(5):
+            orc.binary(0, F32, Ws[li], grads[li][0], -lr, out=Ws[li])
+            orc.binary(0, F32, bs[li], grads[li][1], -lr, out=bs[li])
+        return per_row * bsz
+
+    work, secs, passes = timed(config5b)
+    out["config5b"] = entry(work / secs / 1e12, "TFLOP/s", secs, passes,
+                            f"the fp32 MLP training step on {bsz} of the batch's 8192 rows "
+                            "(GEMM flops of the sampled step over its time)")
+    del Ws, bs
+    # NN layers: layer norm forward and backward on 1024 of the 8192 rows.
+    rows = 1024
+    xs = g.standard_normal((rows, D), dtype=np.float32)
+    dys = g.standard_normal((rows, D), dtype=np.float32)
+    w = g.standard_normal(D, dtype=np.float32)
+    bb = g.standard_normal(D, dtype=np.float32)
+    _, mean, rstd = orc.layer_norm(F32, xs, D, w, bb)
+
+    def nn():
+        orc.layer_norm(F32, xs, D, w, bb)
+        orc.layer_norm_backward(F32, dys, xs, D, mean, rstd, w)
+        return 5 * rows * D * 4
+
+    work, secs, passes = timed(nn)
+    out["nn"] = entry(work / secs / 1e9, "GB/s", secs, passes,
+                      f"layer norm forward and backward on {rows} of the 8192 rows [x {D}], fp32")
+    return out
+
+
 def profile_launches(what: str, lib, ops, dev) -> None:
     """Fixed launch sequences for counter and trace collection under
     rocprofv3 (``--profile``); no timing, no JSON line.
@@ -569,6 +699,9 @@ def main() -> int:
     if not args.no_cpu:
         log("bench: cpu baseline")
         result["cpu_baseline"] = cpu_baseline()
+        if not args.no_suite:
+            log("bench: cpu samples of the suite")
+            result["suite_cpu"] = cpu_suite()
     print(json.dumps(result), flush=True)
     return 0
 
