@@ -37,6 +37,7 @@
 
 #include "device_common.h"
 #include "gemm.h"
+#include "../allocator.h"
 #include "../common.h"
 #include "../runtime.h"
 
@@ -787,6 +788,71 @@ void launch_config(const GemmArgs& whole, hipStream_t stream) {
         launch_chunk<T, BM, BN, WM, WN>(p, stream);
     }
 }
+// Split K for float32 products with too few 128 x 128 tiles to fill the
+// CUs: a single matrix whose K dwarfs M x N (mm 1024^3 has 64 tiles; the
+// Linear(4096, 1024) of a 256-row batch has 16, each running K = 4096 alone
+// on one CU).  S slices of K ride on the kernel's batch index and write
+// float32 partial products into a workspace [S][M][N]; splitk_finish_kernel
+// then adds the slices in slice order -- the result does not depend on
+// timing -- and applies alpha, beta Cin and the epilogue's rounding.
+// S doubles while the tiles times S still fit one block per CU and every
+// slice keeps at least 128 of K, a multiple of the kernel's BK = 32.
+constexpr int kFinishBlock = 256;
+
+int splitk_slices(const GemmArgs& p, int cus) {
+    if (p.batch != 1) return 1;
+    const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+    int s = 1;
+    while (tiles * s * 2 <= cus && p.k % (s * 2 * 32) == 0 && p.k / (s * 2) >= 128) s *= 2;
+    return s;
+}
+
+// c = alpha * sum of the slices (+ beta Cin), the same expressions as the
+// kernels' epilogue; one thread an element, consecutive threads along a row.
+__global__ __launch_bounds__(kFinishBlock) void splitk_finish_kernel(const float* part, int slices, int64_t m,
+                                                               int64_t n, float alpha, float beta,
+                                                               const float* cin, int64_t cin_rs,
+                                                               int64_t cin_cs, float* c, int64_t ldc) {
+    const int64_t mn = m * n;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kFinishBlock + threadIdx.x; i < mn;
+         i += static_cast<int64_t>(gridDim.x) * kFinishBlock) {
+        float acc = part[i];
+        for (int s = 1; s < slices; ++s) acc += part[s * mn + i];
+        const int64_t r = i / n, col = i % n;
+        float v;
+        if (beta == 0.0f) {
+            v = alpha * acc;
+        } else if (cin_rs == 0) {
+            v = fmaf(alpha, acc, beta * cin[col * cin_cs]);
+        } else {
+            v = fmaf(beta, cin[r * cin_rs + col * cin_cs], alpha * acc);
+        }
+        c[r * ldc + col] = v;
+    }
+}
+
+void launch_splitk(const GemmArgs& p, int slices, hipStream_t stream, int device) {
+    const int64_t mn = p.m * p.n;
+    Workspace ws(static_cast<size_t>(slices * mn) * sizeof(float), device);
+    GemmArgs q = p;
+    q.batch = slices;
+    q.k = p.k / slices;
+    q.stride_a = p.trans_a ? q.k * p.lda : q.k;  // slice s starts at k = s q.k
+    q.stride_b = p.trans_b ? q.k : q.k * p.ldb;
+    q.alpha = 1.0f;
+    q.beta = 0.0f;
+    q.cin = nullptr;
+    q.c = ws.get();
+    q.ldc = p.n;
+    q.stride_c = mn;
+    launch_config<float, 128, 128, 2, 2>(q, stream);
+    const int64_t blocks = std::min<int64_t>((mn + kFinishBlock - 1) / kFinishBlock, 4 * int64_t{cu_count(device)});
+    splitk_finish_kernel<<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
+        static_cast<const float*>(ws.get()), slices, p.m, p.n, p.alpha, p.beta,
+        static_cast<const float*>(p.cin), p.cin_rs, p.cin_cs, static_cast<float*>(p.c), p.ldc);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
 // 16-bit types take the big tile when it still gives every CU a block;
 // float32 (bound by its much slower MFMA rate) keeps the small one, whose
 // registers fit without spilling.
@@ -794,6 +860,13 @@ template <typename T>
 void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
+    if constexpr (std::is_same<T, float>::value) {
+        const int slices = splitk_slices(p, cu_count(device));
+        if (slices > 1) {
+            launch_splitk(p, slices, stream, device);
+            return;
+        }
+    }
     if constexpr (sizeof(typename Elem<T>::storage) == 2) {
         if (big::eligible<T>(p, cu_count(device))) {
             big::launch<T>(p, stream);

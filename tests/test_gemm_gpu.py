@@ -242,3 +242,42 @@ def test_gemm_abi_padded_batched(amd, dev, orc, dtype, ta, tb, bt, m, n, k):
     got = out.numpy()
     assert not np.isnan(orc.to_float(got, dtype)).any(), "padding leaked into the product"
     check(orc, got, want, dtype, f"gemm abi {bt}x{m}x{n}x{k} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("cin_kind", ["full", "bias-row"])
+def test_gemm_fp32_split_k(amd, dev, orc, ta, tb, cin_kind):
+    """A float32 product with few 128 x 128 tiles and a long K (256 x 384
+    outputs, K = 4096: 6 tiles) is split over K into float32 partials that are
+    added in slice order: the result matches the float64 product at the fp32
+    bar with alpha = 0.5, beta = 2 and a full Cin or a row-broadcast bias,
+    NaN-padded leading dimensions, and two runs give the same bits."""
+    lib = amd.load()
+    m, n, k, pad, alpha, beta = 256, 384, 4096, 4, 0.5, 2.0
+    a = _padded(orc, (k, m) if ta else (m, k), pad, F32, 7)
+    b = _padded(orc, (n, k) if tb else (k, n), pad, F32, 8)
+    if cin_kind == "full":
+        cin = sample(orc, (m, n), F32, 9)
+        rs, cs = n, 1
+        cin_f = cin
+    else:
+        cin = sample(orc, (n,), F32, 9)
+        rs, cs = 0, 1
+        cin_f = np.broadcast_to(cin, (m, n))
+    da, db, dc = dev.from_numpy(a), dev.from_numpy(b), dev.from_numpy(cin)
+    A = a[:, :m] if ta else a[:, :k]
+    B = b[:, :k] if tb else b[:, :n]
+    A = A.T if ta else A
+    B = B.T if tb else B
+    want = alpha * (A.astype(np.float64) @ B.astype(np.float64)) + beta * cin_f.astype(np.float64)
+    outs = []
+    for _ in range(2):
+        out = dev.empty((m, n), dtype=F32)
+        st = lib.tp_amd_launch_gemm(0, F32, 1, m, n, k, alpha, da.data_ptr, a.shape[-1], 0, int(ta),
+                                    db.data_ptr, b.shape[-1], 0, int(tb), beta, dc.data_ptr, rs, cs, 0,
+                                    out.data_ptr, n, 0)
+        assert st == 0, lib.tp_mlu_last_error()
+        outs.append(out.numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "split-K sum is not deterministic"
+    check(orc, outs[0], want, F32, f"split-K fp32 ta={ta} tb={tb} {cin_kind}")
