@@ -26,11 +26,14 @@
 // K step needs a single barrier.  Operands sit in LDS K-major ([row][k],
 // rows padded by 16 bytes so the 16-byte fragment reads of 16 consecutive
 // rows hit distinct banks).  An operand stored K-major in memory is copied
-// with 16-byte loads; one stored with its M (or N) axis contiguous is loaded
-// as V x 4 blocks (V along M/N, 4 along K) and transposed in registers
-// before its LDS store.  All kernels number their tiles so each of the 8
-// XCDs walks a contiguous range in groups of 8 tile rows, keeping an XCD's A
-// and B panels hot in its own L2.
+// with 16-byte loads; a 16-bit one stored with its M (or N) axis contiguous
+// is loaded as V x 4 blocks (V along M/N, 4 along K) and transposed in
+// registers before its LDS store, a float32 one is kept as it lies
+// ([k][row] tiles, read back one float at a time).  All kernels number their
+// tiles so each of the 8 XCDs walks a contiguous range in groups of 8 tile
+// rows, keeping an XCD's A and B panels hot in its own L2.  A float32
+// product of one matrix with too few tiles to fill the CUs is split over K
+// (launch_splitk).
 
 #include <type_traits>
 #include <utility>
