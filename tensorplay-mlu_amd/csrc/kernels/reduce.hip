@@ -554,12 +554,17 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     const int64_t bx = (inner + cols_per_block - 1) / cols_per_block;
     const int64_t z = outer < 65535 ? outer : 65535;
     const int64_t base_blocks = bx * z;
-    // Two blocks per CU, each with eight 16-byte loads per thread in flight,
-    // keep HBM busy; more chunks would only grow the partials.
-    const int64_t target_blocks = cus * 2;
+    // About one block per CU, each with eight 16-byte loads per thread in
+    // flight: nchunk = round(CUs / column ranges).  Measured on config 3's
+    // dim-0 reductions against the earlier two blocks per CU: X2 [4096,
+    // 32000] bf16 1 chunk 40.8 us against 3 chunks 43.6 us, fp32 2 chunks
+    // 79 us against 5 chunks 85 us; X1 [32768, 4096] bf16 8 chunks 41.1 us
+    // against 16 chunks 43.2 us, fp32 16 or 32 chunks alike.  Fewer chunks
+    // write fewer partials, and the blocks fill the CUs in one even round.
+    const int64_t target_blocks = cus;
     int64_t nchunk = 1;
     if (base_blocks < target_blocks && r >= 64) {
-        nchunk = (target_blocks + base_blocks - 1) / base_blocks;
+        nchunk = (target_blocks + base_blocks / 2) / base_blocks;
         const int64_t max_chunks = r / 32;  // keep >= 32 rows per chunk
         if (nchunk > max_chunks) nchunk = max_chunks > 1 ? max_chunks : 1;
         if (nchunk > 65535) nchunk = 65535;
