@@ -614,8 +614,8 @@ def profile_launches(what: str, lib, ops, dev) -> None:
     gemm:    ten bf16 4096^3 products in each operand layout (A, B
              row-major; B transposed; A transposed; both transposed);
     gemm32:  the same in float32, five products a layout;
-    reduce:  config-3 X1 [32768, 4096] sum and amax over dim -1 and 0, fp32
-             and bf16, five each;
+    reduce:  config-3 X1 [32768, 4096], then X2 [4096, 32000]: sum and amax
+             over dim -1 and 0, fp32 and bf16, five each;
     softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
              X2 [4096, 32000], fp32 and bf16, five each;
     nn:      the NN-layer suite's shapes, fp32 and bf16, five launches of
@@ -651,12 +651,14 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                                               c.data_ptr, K, 0) == 0
     elif what == "reduce":
         g = np.random.default_rng(0)
-        x32 = dev.from_numpy(g.standard_normal((32768, 4096), dtype=np.float32))
-        for x in (x32, ops.to(x32, BF16)):
-            for fn in (ops.sum_dim, ops.amax):
-                for dim in (-1, 0):
-                    for _ in range(5):
-                        fn(x, [dim])
+        for shape in ((32768, 4096), (4096, 32000)):
+            x32 = dev.from_numpy(g.standard_normal(shape, dtype=np.float32))
+            for x in (x32, ops.to(x32, BF16)):
+                for fn in (ops.sum_dim, ops.amax):
+                    for dim in (-1, 0):
+                        for _ in range(5):
+                            fn(x, [dim])
+            del x32, x
     elif what == "softmax":
         g = np.random.default_rng(0)
         for shape in ((32768, 4096), (4096, 32000)):
