@@ -769,26 +769,33 @@ def main() -> int:
         "roofline": roofline,
     }
     if not args.no_suite:
-        log("bench: suite config 2")
-        suite = {"config2": suite_config2(ops, ev, tensors)}
+        def section(name, fn):
+            # A section that fails is reported as such; the headline line
+            # above it still prints.
+            log(f"bench: suite {name}")
+            try:
+                return fn()
+            except Exception as exc:  # noqa: BLE001 - recorded in the JSON line
+                log(f"bench: suite {name} failed: {exc!r}")
+                return {"error": repr(exc)}
+
+        suite = {"config2": section("config 2", lambda: suite_config2(ops, ev, tensors))}
         del tensors
-        log("bench: suite config 3")
-        suite["config3"] = suite_config3(ops, dev, ev)
-        log("bench: suite configs 4 and 5a")
-        suite["config4_5a"] = suite_gemm(ops, dev, ev)
-        log("bench: suite config 5b")
-        suite["config5b"] = suite_config5b(ops, dev, ev)
-        log("bench: suite NN layers")
-        suite["nn"] = suite_nn(ops, dev, ev)
-        log("bench: the reference README's rows")
-        suite["readme_rows"] = suite_readme(ops, dev, ev, lib)
+        suite["config3"] = section("config 3", lambda: suite_config3(ops, dev, ev))
+        suite["config4_5a"] = section("configs 4 and 5a", lambda: suite_gemm(ops, dev, ev))
+        suite["config5b"] = section("config 5b", lambda: suite_config5b(ops, dev, ev))
+        suite["nn"] = section("NN layers", lambda: suite_nn(ops, dev, ev))
+        suite["readme_rows"] = section("the reference README's rows", lambda: suite_readme(ops, dev, ev, lib))
         result["suite"] = suite
     if not args.no_cpu:
         log("bench: cpu baseline")
         result["cpu_baseline"] = cpu_baseline()
         if not args.no_suite:
             log("bench: cpu samples of the suite")
-            result["suite_cpu"] = cpu_suite()
+            try:
+                result["suite_cpu"] = cpu_suite()
+            except Exception as exc:  # noqa: BLE001 - recorded in the JSON line
+                result["suite_cpu"] = {"error": repr(exc)}
     print(json.dumps(result), flush=True)
     return 0
 
