@@ -97,6 +97,14 @@ struct Mfma<float> {
 
 constexpr int kGroupM = 8;
 
+// Stores of C bypass the caches' normal retention (non-temporal): a large
+// product's output then does not evict the A and B panels later tiles read
+// (bf16 linear 8192 x 4096 x 11008: 704-713 -> 656-670 us).
+template <typename S>
+__device__ __forceinline__ void put_c(S* dst, S v) {
+    __builtin_nontemporal_store(v, dst);
+}
+
 __device__ __forceinline__ uint32_t component(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
@@ -372,7 +380,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             if (rbase + 8 * g + r < p.m) {
-                                cp[r * p.ldc] = Elem<T>::store(p.alpha * acc[i][j][4 * g + r]);
+                                put_c(&cp[r * p.ldc], Elem<T>::store(p.alpha * acc[i][j][4 * g + r]));
                             }
                         }
                         cp += 8 * p.ldc;
@@ -385,7 +393,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             if (rbase + 8 * g + r < p.m) {
-                                cp[r * p.ldc] = Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c));
+                                put_c(&cp[r * p.ldc], Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c)));
                             }
                         }
                         cp += 8 * p.ldc;
@@ -398,8 +406,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
                         for (int r = 0; r < 4; ++r) {
                             if (rbase + 8 * g + r < p.m) {
                                 const float c = Elem<T>::load(ci[r * p.cin_rs]);
-                                cp[r * p.ldc] =
-                                    Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r]));
+                                put_c(&cp[r * p.ldc],
+                                      Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r])));
                             }
                         }
                         cp += 8 * p.ldc;
@@ -661,7 +669,7 @@ __global__ __launch_bounds__(WM * WN * kWave, (WM * WN) / 4) void gemm_big_kerne
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) cp[r * p.ldc] = Elem<T>::store(p.alpha * acc[i][j][4 * g + r]);
+                    for (int r = 0; r < 4; ++r) put_c(&cp[r * p.ldc], Elem<T>::store(p.alpha * acc[i][j][4 * g + r]));
                     cp += 8 * p.ldc;
                 }
             } else if (p.cin_rs == 0) {
@@ -669,7 +677,7 @@ __global__ __launch_bounds__(WM * WN * kWave, (WM * WN) / 4) void gemm_big_kerne
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) cp[r * p.ldc] = Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c));
+                    for (int r = 0; r < 4; ++r) put_c(&cp[r * p.ldc], Elem<T>::store(fmaf(p.alpha, acc[i][j][4 * g + r], c)));
                     cp += 8 * p.ldc;
                 }
             } else {
@@ -679,7 +687,7 @@ __global__ __launch_bounds__(WM * WN * kWave, (WM * WN) / 4) void gemm_big_kerne
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float c = Elem<T>::load(ci[r * p.cin_rs]);
-                        cp[r * p.ldc] = Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r]));
+                        put_c(&cp[r * p.ldc], Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[i][j][4 * g + r])));
                     }
                     cp += 8 * p.ldc;
                     ci += 8 * p.cin_rs;
