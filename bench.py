@@ -28,7 +28,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,gemm32,reduce,softmax,nn}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,gemm32,reduce,softmax,nn,mlp}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -614,6 +614,9 @@ def profile_launches(what: str, lib, ops, dev) -> None:
     gemm:    ten bf16 4096^3 products in each operand layout (A, B
              row-major; B transposed; A transposed; both transposed);
     gemm32:  the same in float32, five products a layout;
+    mlp:     three config-5b training steps (fp32 MLP, batch 8192, four
+             Linear(4096, 4096) + ReLU, Linear(4096, 1000), log_softmax, NLL
+             through mul + sum, backward, SGD) after one untimed step;
     reduce:  config-3 X1 [32768, 4096], then X2 [4096, 32000]: sum and amax
              over dim -1 and 0, fp32 and bf16, five each;
     softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
@@ -697,6 +700,18 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                 ops.nll_loss(logp, tgt, None, 1)
                 ops.nll_loss_backward(one, logp, tgt, None, 1, -100, total)
             del x, dy, w, b, mean, rstd, mask, table, logp, total
+    elif what == "mlp":
+        wl = importlib.import_module("tensorplay-mlu_amd.workloads")
+        ws, bs = wl.MLP.host_init(4096, 4, 4096, 1000, seed=0)
+        model = wl.MLP.to_device(ws, bs)
+        del ws, bs
+        g = np.random.default_rng(100)
+        x = dev.from_numpy(g.standard_normal((8192, 4096), dtype=np.float32))
+        onehot = np.zeros((8192, 1000), np.float32)
+        onehot[np.arange(8192), g.integers(0, 1000, 8192)] = 1.0
+        oh = dev.from_numpy(onehot)
+        for _ in range(4):
+            wl.mlp_step(ops, model, x, oh, 1e-3)
     else:
         raise SystemExit(f"unknown --profile {what}")
     assert lib.tp_amd_synchronize(0) == 0
@@ -710,7 +725,7 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "softmax", "nn"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "softmax", "nn", "mlp"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
