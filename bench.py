@@ -477,6 +477,63 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 8):
                       "OpenMP; TensorPlay's CPU path is not installed)"}
 
 
+def _torch_cpu(cores: int):
+    """torch on the host CPU with the oracle's thread count, or None."""
+    try:
+        import torch
+    except ImportError:
+        return None
+    torch.set_num_threads(cores)
+    return torch
+
+
+def torch_cpu_mm(cores: int, seconds: float) -> dict:
+    """A calibration line beside the oracle's GEMM figure: torch's CPU matmul
+    (its BLAS, float32) on the whole 4096^3 mm, TFLOP/s; not TensorPlay's
+    CPU path."""
+    torch = _torch_cpu(cores)
+    if torch is None:
+        return {"error": "torch not importable"}
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(4096, 4096, generator=g)
+    b = torch.randn(4096, 4096, generator=g)
+    torch.mm(a, b)
+    n, t0 = 0, time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        torch.mm(a, b)
+        n += 1
+    secs = time.perf_counter() - t0
+    return {"value": float(f"{2 * 4096 ** 3 * n / secs / 1e12:.4g}"), "unit": "TFLOP/s", "cores": cores,
+            "kind": "calibration", "sample": f"torch.mm fp32 4096^3 on the host CPU, {n} call(s)"}
+
+
+def torch_cpu_config3(cores: int, seconds: float) -> dict:
+    """A calibration line beside the oracle's config-3 figure: torch on the
+    host CPU running X1's four reductions over dim -1 and 0 and softmax /
+    log_softmax forward on the whole X1 [32768, 4096] fp32, GB/s of
+    algorithmic bytes; not TensorPlay's CPU path."""
+    torch = _torch_cpu(cores)
+    if torch is None:
+        return {"error": "torch not importable"}
+    x = torch.randn(32768, 4096, generator=torch.Generator().manual_seed(0)) * 2.0
+    n_bytes = x.numel() * 4
+
+    def one():
+        for dim in (-1, 0):
+            x.sum(dim), x.mean(dim), x.amax(dim), x.amin(dim)
+        torch.softmax(x, -1), torch.log_softmax(x, -1)
+        return 8 * n_bytes + 2 * 2 * n_bytes
+
+    work, n, t0 = 0, 0, time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        work += one()
+        n += 1
+    secs = time.perf_counter() - t0
+    return {"value": float(f"{work / secs / 1e9:.4g}"), "unit": "GB/s", "cores": cores, "kind": "calibration",
+            "sample": f"torch CPU: sum/mean/amax/amin over dim -1 and 0 and softmax/log_softmax forward on "
+                      f"X1 [32768, 4096] fp32, {n} pass(es)"}
+
+
 def cpu_suite(seconds_each: float = 3.0) -> dict:
     """CPU figures beside the suite's sections, in each section's unit: the C
     oracle (float64 arithmetic, OpenMP over the host's cores) on a bounded
@@ -527,6 +584,7 @@ def cpu_suite(seconds_each: float = 3.0) -> dict:
     out["config3"] = entry(work / secs / 1e9, "GB/s", secs, passes,
                            "sum/mean/amax/amin over dim -1 and 0, softmax and log_softmax forward "
                            f"and backward on {rows} of X1's 32768 rows [x 4096], fp32 and bf16")
+    out["config3"]["torch_cpu_calibration"] = torch_cpu_config3(cores, seconds_each)
     del prep
     # Config 4: 64 rows of the 4096^3 products, fp32 and bf16 (fp32 accumulation).
     m, K = 64, 4096
@@ -544,6 +602,7 @@ def cpu_suite(seconds_each: float = 3.0) -> dict:
     work, secs, passes = timed(config4)
     out["config4"] = entry(work / secs / 1e12, "TFLOP/s", secs, passes,
                            f"mm {m}x{K}x{K} ({m} of the 4096 rows of config 4's mm), fp32 and bf16")
+    out["config4"]["torch_cpu_calibration"] = torch_cpu_mm(cores, seconds_each)
     del ops4
     # Config 5b: the MLP training step on 32 of the batch's 8192 rows (four
     # Linear(4096, 4096) + ReLU, Linear(4096, 1000), log_softmax, NLL through
