@@ -584,7 +584,7 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
         TP_AMD_HIP_CHECK(hipGetLastError());
         return;
     }
-    // Rows are split only when bx * outer < 2 * cus, so one arrival counter
+    // Rows are split only when bx * outer < cus, so one arrival counter
     // per column range always fits.
     TP_AMD_CHECK(outer * bx <= kMaxColCounters, "column reduction: ", outer * bx,
                  " column ranges exceed the arrival counters");
