@@ -69,6 +69,32 @@ __device__ __forceinline__ float row_sum(float v, float* scratch) {
     return v;
 }
 
+// Two sums at once, each added in the same order as `row_sum` (so the same
+// bits), with one pair of barriers; scratch holds 2 floats a wave.
+template <int WAVES>
+__device__ __forceinline__ void row_sum2(float& a, float& c, float* scratch) {
+    a = wave_allreduce(a, Plus{});
+    c = wave_allreduce(c, Plus{});
+    if constexpr (WAVES > 1) {
+        const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+        const int first = (wave / WAVES) * WAVES;
+        __syncthreads();  // the previous use of scratch is done
+        if (lane == 0) {
+            scratch[2 * wave] = a;
+            scratch[2 * wave + 1] = c;
+        }
+        __syncthreads();
+        float ta = 0.0f, tc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            ta += scratch[2 * (first + w)];
+            tc += scratch[2 * (first + w) + 1];
+        }
+        a = ta;
+        c = tc;
+    }
+}
+
 template <typename T, int VPT>
 __device__ __forceinline__ void load_params(const S_<T>* p, float (&out)[VPT][Packet<T>::N],
                                             int tid, int threads, int64_t npk, float fallback) {
@@ -232,7 +258,7 @@ __global__ __launch_bounds__(GROUPS * WAVES * kWave) void layer_norm_backward_ro
     constexpr int N = Packet<T>::N;
     constexpr int kThreads = WAVES * kWave;
     extern __shared__ float fold[];
-    __shared__ float scratch[GROUPS * WAVES];
+    __shared__ float scratch[2 * GROUPS * WAVES];
     const int tid = threadIdx.x % kThreads;
     const int group = threadIdx.x / kThreads;
     const int64_t npk = D / N;
@@ -294,8 +320,9 @@ __global__ __launch_bounds__(GROUPS * WAVES * kWave) void layer_norm_backward_ro
                 pb[k][j] += dv[j];
             }
         }
-        a = row_sum<WAVES>(a, scratch) * inv_d;
-        c = row_sum<WAVES>(c, scratch) * inv_d;
+        row_sum2<WAVES>(a, c, scratch);
+        a *= inv_d;
+        c *= inv_d;
         const bool write = dx != nullptr && row < rows;
         const Rsrc rdx = buffer_over(dx + (write ? row * D : 0), write ? row_bytes : 0);
 #pragma unroll
