@@ -5,12 +5,13 @@
 // * inner == 1 (row reductions): a wavefront (or, for long rows, a whole
 //   256-thread block) reduces one row segment with 16-byte packet loads,
 //   then combines across lanes with DPP/shuffle steps and across waves in
-//   LDS.  When there are too few rows to fill 256 CUs, rows are split into
-//   segments whose float32 partials a second pass combines.
+//   LDS.  When there are too few rows to fill 256 CUs (a whole-tensor sum),
+//   rows are split into segments of one block each, and the last block of a
+//   row to finish folds the row's float32 partials in the same launch.
 // * inner > 1 (column reductions, e.g. dim 0 of [32768, 4096]): lanes walk
 //   the contiguous inner axis with packets, four row groups per block share
-//   the rows of a chunk, and chunks of rows are spread over the grid; a
-//   second pass combines the chunk partials.
+//   the rows of a chunk, and chunks of rows are spread over the grid; the
+//   last block of a column range folds the chunk partials in the same launch.
 // Arithmetic is float32.  amax/amin skip NaN inputs and order -0 below +0,
 // so every evaluation order gives the same bits.
 
@@ -153,15 +154,14 @@ __device__ __forceinline__ float finish(float v, int64_t count, bool final_pass)
 __device__ __forceinline__ uint4 splat(uint32_t w) { return make_uint4(w, w, w, w); }
 
 // One thread's share of packets [pb, pe) of a row segment: packets
-// pb + tid, pb + tid + THREADS, ...  Loads go out in batches of U, the
+// pb + tid, pb + tid + THREADS, ...  Loads go out in batches of U (4 by default), the
 // batch's out-of-range slots padded with a value that leaves the result
 // unchanged, so every batch's loads are in flight together.  Float combine
 // in element order.
-template <typename Tin, int OP, int THREADS>
+template <typename Tin, int OP, int THREADS, int U = 4>
 __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p, int64_t pb,
                                            int64_t pe, int tid) {
     constexpr int N = Packet<Tin>::N;
-    constexpr int U = 4;
     // Zeros add nothing; NaN is skipped by amax / amin.
     constexpr uint32_t kPad = kMinMax<OP> ? (N == 4 ? 0x7fc00000u : (std::is_same_v<Tin, bf16_t>
                                                                           ? 0x7fc07fc0u
@@ -189,11 +189,10 @@ __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p,
 // The same share for amax / amin on integer keys (NaN when a NaN wins or the
 // share is empty).  The padding is the NaN pattern whose key loses to every
 // value.
-template <typename Tin, int OP, int THREADS>
+template <typename Tin, int OP, int THREADS, int U = 4>
 __device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, int64_t pb,
                                           int64_t pe, int tid) {
     constexpr int N = Packet<Tin>::N;
-    constexpr int U = 4;
     using K = KeyOps<OP>;
     constexpr bool kWide = sizeof(typename Elem<Tin>::storage) == 4;
     constexpr uint32_t kPad = K::kMax ? 0xffffffffu : (kWide ? 0x7fffffffu : 0x7fff7fffu);
@@ -268,6 +267,91 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
         }
     } else {
         if (lane == 0 && seg < nsegs) out[seg] = Elem<Tout>::store(finish<OP>(acc, count, final_pass));
+    }
+}
+
+// The block's value of `v` (combined over its waves in wave order), in
+// thread 0.
+template <int OP>
+__device__ __forceinline__ float block_reduce(float v) {
+    __shared__ float waves[kBlock / kWave];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    v = lane_reduce<OP>(v);
+    if (lane == 0) waves[wave] = v;
+    __syncthreads();
+    if (wave == 0) {
+        v = lane < kBlock / kWave ? waves[lane] : Combine<OP>::identity();
+        v = lane_reduce<OP>(v);
+    }
+    return v;
+}
+
+// Few long rows (a whole-tensor sum, a loss over all logits): each row is
+// split into nseg segments, one 256-thread block a segment, and the partials
+// are folded in the same launch.  Block s reduces segment s (row s / nseg,
+// elements [(s % nseg) * chunk, +chunk)), stores its float32 partial with an
+// agent-coherent store, waits for the store to complete, and counts its
+// arrival in row_counters[row]; the row's last block reads the nseg partials
+// back (agent-coherent loads) and folds them in a fixed order -- thread t
+// takes partials t, t + 256, ... in turn, then the block combines its waves
+// in order -- so the bits do not depend on which block arrived last.  It
+// writes the result and resets the counter for the next launch (device
+// globals start zeroed when the code object loads).
+//
+// Ordering: the fold relies on gfx950's memory system, not on a C++ release
+// / acquire pair.  An agent-scope store is issued with sc1 set and written
+// through to the device-coherent level (past the non-coherent per-XCD L2),
+// and s_waitcnt vmcnt(0) returns only once that write is acknowledged; the
+// counter's atomic add is issued after it, and the agent-scope loads of the
+// last block (sc1 set) read the coherent level.  An agent-scope release
+// would instead write back this XCD's whole L2 in every block.
+constexpr int64_t kMaxRowCounters = 4096;
+__device__ unsigned int row_counters[kMaxRowCounters];
+
+template <typename Tin, int OP, bool VEC>
+__global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
+    const typename Elem<Tin>::storage* x, typename Elem<Tin>::storage* out, float* partial,
+    int64_t r, int64_t chunk, int64_t nseg) {
+    constexpr int N = VEC ? Packet<Tin>::N : 1;
+    const int64_t seg = blockIdx.x;
+    const int64_t row = seg / nseg, part = seg - row * nseg;
+    const int64_t begin = part * chunk;
+    const int64_t end = begin + chunk < r ? begin + chunk : r;
+    const typename Elem<Tin>::storage* p = x + row * r;
+    const int tid = threadIdx.x;
+    float acc = Combine<OP>::identity();
+    if constexpr (VEC) {
+        const int64_t pb = begin / N, pe = end / N;
+        if constexpr (kMinMax<OP>) {
+            acc = row_keys<Tin, OP, kBlock, 8>(p, pb, pe, tid);
+            if (acc != acc) acc = row_exact<Tin, OP, kBlock, 8>(p, pb, pe, tid);
+        } else {
+            acc = row_exact<Tin, OP, kBlock, 8>(p, pb, pe, tid);
+        }
+    } else {
+        for (int64_t j = begin + tid; j < end; j += kBlock) {
+            acc = Combine<OP>::apply(acc, Elem<Tin>::load(p[j]));
+        }
+    }
+    acc = block_reduce<OP>(acc);
+    __shared__ bool last;
+    if (tid == 0) {
+        __hip_atomic_store(&partial[seg], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(&row_counters[row], 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == nseg - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    const float* q = partial + row * nseg;
+    float v = Combine<OP>::identity();
+    for (int64_t k = tid; k < nseg; k += kBlock) {
+        v = Combine<OP>::apply(v, __hip_atomic_load(q + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    v = block_reduce<OP>(v);
+    if (tid == 0) {
+        out[row] = Elem<Tin>::store(finish<OP>(v, r, true));
+        __hip_atomic_store(&row_counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -479,9 +563,37 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
     }
 }
 
+// Device memory for the float32 partials of a split reduction: a caller's
+// buffer of `floats` elements (the allocation-free entry point), or, when
+// `ptr` is null, a workspace from the caching allocator.
+struct Scratch {
+    float* ptr = nullptr;
+    int64_t floats = 0;
+};
+
+class Partials {
+public:
+    Partials(const Scratch& scratch, int64_t floats, int device) {
+        if (scratch.ptr != nullptr) {
+            TP_AMD_CHECK(floats <= scratch.floats, "reduction needs ", floats * 4,
+                         " bytes of partials, more than the ", scratch.floats * 4,
+                         "-byte static scratch; use tp_amd_launch_reduce");
+            ptr_ = scratch.ptr;
+        } else {
+            ws_ = Workspace(static_cast<size_t>(floats) * sizeof(float), device);
+            ptr_ = static_cast<float*>(ws_.get());
+        }
+    }
+    float* get() const { return ptr_; }
+
+private:
+    Workspace ws_;
+    float* ptr_ = nullptr;
+};
+
 template <typename T, int OP>
 void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const void* xv,
-                  void* outv) {
+                  void* outv, const Scratch& scratch) {
     using S = typename Elem<T>::storage;
     const S* x = static_cast<const S*>(xv);
     S* out = static_cast<S*>(outv);
@@ -490,61 +602,54 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     constexpr int N = Packet<T>::N;
     if (inner == 1) {
         const bool vec = r % N == 0 && aligned16(x);
-        // Enough independent rows fill the chip; otherwise split the rows.
-        const int64_t target_segs = cus * 16;
-        int64_t nseg = 1;
-        if (outer < target_segs && r >= 8192) {
-            nseg = (target_segs + outer - 1) / outer;
-            const int64_t max_seg = r / 2048;  // keep segments >= 2048 elements
-            if (nseg > max_seg) nseg = max_seg > 1 ? max_seg : 1;
+        // Fewer rows than fill the chip, and long ones: split each row into
+        // segments of at least 4096 elements, about eight blocks per CU in
+        // all, and fold the partials in the same launch.
+        if (outer < cus * 16 && r >= 8192) {
+            int64_t nseg = (cus * 8 + outer - 1) / outer;
+            const int64_t max_seg = r / 4096;
+            if (nseg > max_seg) nseg = max_seg;
+            int64_t chunk = (r + nseg - 1) / nseg;
+            if (vec) chunk = (chunk + N - 1) / N * N;
+            nseg = (r + chunk - 1) / chunk;
+            if (nseg > 1) {
+                TP_AMD_CHECK(outer <= kMaxRowCounters, "row reduction: ", outer,
+                             " rows exceed the arrival counters");
+                const int64_t nsegs = outer * nseg;
+                Partials partial(scratch, nsegs, device);
+                if (vec) {
+                    reduce_rows_fused_kernel<T, OP, true>
+                        <<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(x, out, partial.get(), r, chunk, nseg);
+                } else {
+                    reduce_rows_fused_kernel<T, OP, false>
+                        <<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(x, out, partial.get(), r, chunk, nseg);
+                }
+                TP_AMD_HIP_CHECK(hipGetLastError());
+                return;
+            }
         }
-        int64_t chunk = (r + nseg - 1) / nseg;
-        if (vec) chunk = (chunk + N - 1) / N * N;
-        nseg = (r + chunk - 1) / chunk;
-        const int64_t nsegs = outer * nseg;
-        // Four waves share a segment of 4096 elements or more; amax / amin of
-        // 16-bit storage (integer keys) run best one wave a segment up to
-        // 16 KB (measured on 4096-element bf16 rows: 40 us against 45-49 us).
+        // One segment per row.  Four waves share a row of 4096 elements or
+        // more; amax / amin of 16-bit storage (integer keys) run best one
+        // wave a row up to 16 KB (measured on 4096-element bf16 rows: 40 us
+        // against 45-49 us).
         const bool key16 = kMinMax<OP> && sizeof(S) == 2;
-        const bool long_rows = key16 ? chunk * 2 >= 16384 : chunk >= 4096;
-        auto launch_rows = [&](auto waves_tag, auto vec_tag, auto* dst, bool final_pass) {
+        const bool long_rows = key16 ? r * 2 >= 16384 : r >= 4096;
+        auto launch_rows = [&](auto waves_tag, auto vec_tag) {
             constexpr int W = decltype(waves_tag)::value;
             constexpr bool V = decltype(vec_tag)::value;
-            using Tout = std::remove_pointer_t<decltype(dst)>;
             constexpr int per_block = (kBlock / kWave) / W;
-            const int64_t blocks = (nsegs + per_block - 1) / per_block;
-            using TO = std::conditional_t<std::is_same<Tout, float>::value, float, T>;
-            reduce_rows_kernel<T, TO, OP, W, V><<<blocks, kBlock, 0, st>>>(
-                x, reinterpret_cast<typename Elem<TO>::storage*>(dst), nsegs, r, chunk, nseg,
-                final_pass, r);
+            const int64_t blocks = (outer + per_block - 1) / per_block;
+            reduce_rows_kernel<T, T, OP, W, V><<<blocks, kBlock, 0, st>>>(x, out, outer, r, r, 1, true, r);
         };
         using One = std::integral_constant<int, 1>;
         using Four = std::integral_constant<int, 4>;
         using Yes = std::true_type;
         using No = std::false_type;
-        if (nseg == 1) {
-            if (long_rows) {
-                vec ? launch_rows(Four{}, Yes{}, out, true) : launch_rows(Four{}, No{}, out, true);
-            } else {
-                vec ? launch_rows(One{}, Yes{}, out, true) : launch_rows(One{}, No{}, out, true);
-            }
-            TP_AMD_HIP_CHECK(hipGetLastError());
-            return;
-        }
-        Workspace ws(static_cast<size_t>(nsegs) * sizeof(float), device);
-        float* partial = static_cast<float*>(ws.get());
         if (long_rows) {
-            vec ? launch_rows(Four{}, Yes{}, partial, false)
-                : launch_rows(Four{}, No{}, partial, false);
+            vec ? launch_rows(Four{}, Yes{}) : launch_rows(Four{}, No{});
         } else {
-            vec ? launch_rows(One{}, Yes{}, partial, false)
-                : launch_rows(One{}, No{}, partial, false);
+            vec ? launch_rows(One{}, Yes{}) : launch_rows(One{}, No{});
         }
-        TP_AMD_HIP_CHECK(hipGetLastError());
-        // Second pass: one wave per row over its nseg float32 partials.
-        const int64_t blocks = (outer + (kBlock / kWave) - 1) / (kBlock / kWave);
-        reduce_rows_kernel<float, T, OP, 1, false><<<blocks, kBlock, 0, st>>>(
-            partial, out, outer, nseg, nseg, 1, true, r);
         TP_AMD_HIP_CHECK(hipGetLastError());
         return;
     }
@@ -588,8 +693,8 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     // per column range always fits.
     TP_AMD_CHECK(outer * bx <= kMaxColCounters, "column reduction: ", outer * bx,
                  " column ranges exceed the arrival counters");
-    Workspace ws(static_cast<size_t>(outer) * nchunk * inner * sizeof(float), device);
-    float* partial = static_cast<float*>(ws.get());
+    Partials partials(scratch, outer * nchunk * inner, device);
+    float* partial = partials.get();
     // One launch: the last block of each column range folds the partials.
     if (vec) {
         reduce_cols_kernel<T, float, OP, true, true>
@@ -603,22 +708,41 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
 
 template <typename T>
 void reduce_dispatch_op(int device, int op, int64_t outer, int64_t r, int64_t inner,
-                        const void* x, void* out) {
+                        const void* x, void* out, const Scratch& scratch) {
     switch (op) {
         case TP_AMD_REDUCE_SUM:
-            reduce_typed<T, TP_AMD_REDUCE_SUM>(device, outer, r, inner, x, out);
+            reduce_typed<T, TP_AMD_REDUCE_SUM>(device, outer, r, inner, x, out, scratch);
             break;
         case TP_AMD_REDUCE_MEAN:
-            reduce_typed<T, TP_AMD_REDUCE_MEAN>(device, outer, r, inner, x, out);
+            reduce_typed<T, TP_AMD_REDUCE_MEAN>(device, outer, r, inner, x, out, scratch);
             break;
         case TP_AMD_REDUCE_AMAX:
-            reduce_typed<T, TP_AMD_REDUCE_AMAX>(device, outer, r, inner, x, out);
+            reduce_typed<T, TP_AMD_REDUCE_AMAX>(device, outer, r, inner, x, out, scratch);
             break;
         case TP_AMD_REDUCE_AMIN:
-            reduce_typed<T, TP_AMD_REDUCE_AMIN>(device, outer, r, inner, x, out);
+            reduce_typed<T, TP_AMD_REDUCE_AMIN>(device, outer, r, inner, x, out, scratch);
             break;
         default: TP_AMD_CHECK(false, "unknown reduce op ", op);
     }
+}
+
+int launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r, int64_t inner,
+                  const void* x, void* out, const Scratch& scratch) {
+    return guarded([&] {
+        TP_AMD_CHECK(outer >= 0 && r >= 0 && inner >= 0, "negative reduce extent");
+        if (outer == 0 || inner == 0) return;
+        TP_AMD_CHECK(r > 0, "reduce over an empty axis: the caller fills the result");
+        const int index = resolve_device(device);
+        DeviceGuard guard(index);
+        switch (dtype) {
+            case TP_AMD_FLOAT32: reduce_dispatch_op<float>(index, op, outer, r, inner, x, out, scratch); break;
+            case TP_AMD_BFLOAT16: reduce_dispatch_op<bf16_t>(index, op, outer, r, inner, x, out, scratch); break;
+            case TP_AMD_FLOAT16: reduce_dispatch_op<f16_t>(index, op, outer, r, inner, x, out, scratch); break;
+            default:
+                TP_AMD_CHECK(false, "reductions take float32, float16 or bfloat16, got ",
+                             dtype_name(dtype));
+        }
+    });
 }
 
 }  // namespace
@@ -631,21 +755,7 @@ extern "C" {
 
 int tp_amd_launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r,
                          int64_t inner, const void* x, void* out) {
-    return guarded([&] {
-        TP_AMD_CHECK(outer >= 0 && r >= 0 && inner >= 0, "negative reduce extent");
-        if (outer == 0 || inner == 0) return;
-        TP_AMD_CHECK(r > 0, "reduce over an empty axis: the caller fills the result");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
-        switch (dtype) {
-            case TP_AMD_FLOAT32: reduce_dispatch_op<float>(index, op, outer, r, inner, x, out); break;
-            case TP_AMD_BFLOAT16: reduce_dispatch_op<bf16_t>(index, op, outer, r, inner, x, out); break;
-            case TP_AMD_FLOAT16: reduce_dispatch_op<f16_t>(index, op, outer, r, inner, x, out); break;
-            default:
-                TP_AMD_CHECK(false, "reductions take float32, float16 or bfloat16, got ",
-                             dtype_name(dtype));
-        }
-    });
+    return launch_reduce(device, op, dtype, outer, r, inner, x, out, Scratch{});
 }
 
 }  // extern "C"

@@ -92,3 +92,27 @@ def assert_normwise(got: np.ndarray, want: np.ndarray, dtype: int, scale: float 
     tol = NORM_TOL[dtype] * ref * 10
     assert err <= tol, f"{what}: max error {err} > tolerance {tol}"
     return err
+
+
+def assert_sum(got: np.ndarray, want: np.ndarray, dtype: int, what: str = "", count: int = 1) -> float:
+    """Sums and means: the kernels add in float32 and round once to the
+    storage dtype, the oracle adds in float64 and rounds once, so the
+    reference's norm-wise rule holds at scale 1.  A mean is compared on its
+    sum's scale (both sides times ``count``, the number of reduced elements),
+    where a 16-bit mean of zero-mean data is not lost under the rule's floor
+    of 1.  The data must make the check able to fail: the tolerance has to
+    sit below max |want|, so a result of zeros (or any result off by the
+    whole answer) is caught."""
+    g = as_float(got, dtype).astype(np.float64) * count
+    w = as_float(want, dtype).astype(np.float64) * count
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    if w.size == 0:
+        return 0.0
+    peak = float(np.max(np.abs(w)))
+    tol = NORM_TOL[dtype] * max(peak, 1.0) * 10
+    assert np.isfinite(peak) and tol < peak, (
+        f"{what}: tolerance {tol} >= max |want| {peak}; a zero result would pass -- use data "
+        "with larger sums")
+    err = float(np.max(np.abs(g - w)))
+    assert err <= tol, f"{what}: max error {err} > tolerance {tol}"
+    return err
