@@ -104,6 +104,23 @@ typedef enum tp_amd_reduce_op {
 int tp_amd_launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r,
                          int64_t inner, const void* x, void* out);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The same reduction as tp_amd_launch_reduce, with the
+ * same kernels and bit-identical results, but the float32 partials of a split
+ * reduction live in a static device array of
+ * tp_amd_reduce_noalloc_scratch_bytes() bytes per GPU (1 MiB, held until the
+ * process ends) instead of coming from the caching allocator; nothing is
+ * allocated or freed.  A reduction that would need more partials than that
+ * returns TP_AMD_ERROR.  Every call on one GPU shares that GPU's array, so
+ * calls that overlap on one device (other streams, other processes' copies
+ * aside) race; calls on the library's single stream are ordered and safe. */
+int tp_amd_launch_reduce_noalloc(int device, int op, int dtype, int64_t outer, int64_t r,
+                                 int64_t inner, const void* x, void* out);
+
+/* Size in bytes of the static partials array of tp_amd_launch_reduce_noalloc. */
+size_t tp_amd_reduce_noalloc_scratch_bytes(void);
+
 /* Replaces cnnlSoftmaxForward (ReduceKernels.cpp:171-183): x, y dense
  * [outer, dim, inner] of ``dtype``; softmax (log_softmax when ``log``) along
  * the middle axis, float32 arithmetic. */

@@ -125,6 +125,8 @@ PROTOTYPES = {
     "tp_amd_launch_unary": (i32, [i32, i32, i32, i32, I64P, VP, I64P, VP, f32]),
     "tp_amd_launch_activation_backward": (i32, [i32, i32, i32, i64, VP, VP, VP, f32]),
     "tp_amd_launch_reduce": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
+    "tp_amd_launch_reduce_noalloc": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
+    "tp_amd_reduce_noalloc_scratch_bytes": (C.c_size_t, []),
     "tp_amd_launch_softmax": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
     "tp_amd_launch_softmax_backward": (i32, [i32, i32, i32, i64, i64, i64, VP, VP, VP]),
     "tp_amd_launch_gemm": (i32, [i32, i32, i64, i64, i64, i64, f32, VP, i64, i64, i32, VP, i64,

@@ -19,6 +19,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
 
 #include "device_common.h"
@@ -726,14 +727,36 @@ void reduce_dispatch_op(int device, int op, int64_t outer, int64_t r, int64_t in
     }
 }
 
+// Allocation-free partials: a static device array, one per GPU, holding the
+// split reductions' float32 partials (at most kScratchFloats).  Host code
+// never passes `reduce_scratch` itself to a kernel: its device address on
+// each GPU comes from hipGetSymbolAddress, taken once per device with that
+// device current.
+constexpr int64_t kScratchFloats = int64_t{1} << 18;  // 1 MiB
+__device__ __attribute__((aligned(256))) float reduce_scratch[kScratchFloats];
+
+Scratch static_scratch(int device) {
+    static std::mutex mutex;
+    static float* ptrs[kMaxDevices] = {};
+    TP_AMD_CHECK(device >= 0 && device < kMaxDevices, "device ", device, " out of range");
+    std::lock_guard<std::mutex> lock(mutex);
+    if (ptrs[device] == nullptr) {
+        void* p = nullptr;
+        TP_AMD_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(reduce_scratch)));
+        ptrs[device] = static_cast<float*>(p);
+    }
+    return Scratch{ptrs[device], kScratchFloats};
+}
+
 int launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r, int64_t inner,
-                  const void* x, void* out, const Scratch& scratch) {
+                  const void* x, void* out, bool no_alloc) {
     return guarded([&] {
         TP_AMD_CHECK(outer >= 0 && r >= 0 && inner >= 0, "negative reduce extent");
         if (outer == 0 || inner == 0) return;
         TP_AMD_CHECK(r > 0, "reduce over an empty axis: the caller fills the result");
         const int index = resolve_device(device);
         DeviceGuard guard(index);
+        const Scratch scratch = no_alloc ? static_scratch(index) : Scratch{};
         switch (dtype) {
             case TP_AMD_FLOAT32: reduce_dispatch_op<float>(index, op, outer, r, inner, x, out, scratch); break;
             case TP_AMD_BFLOAT16: reduce_dispatch_op<bf16_t>(index, op, outer, r, inner, x, out, scratch); break;
@@ -755,7 +778,16 @@ extern "C" {
 
 int tp_amd_launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r,
                          int64_t inner, const void* x, void* out) {
-    return launch_reduce(device, op, dtype, outer, r, inner, x, out, Scratch{});
+    return launch_reduce(device, op, dtype, outer, r, inner, x, out, false);
+}
+
+int tp_amd_launch_reduce_noalloc(int device, int op, int dtype, int64_t outer, int64_t r,
+                                 int64_t inner, const void* x, void* out) {
+    return launch_reduce(device, op, dtype, outer, r, inner, x, out, true);
+}
+
+size_t tp_amd_reduce_noalloc_scratch_bytes(void) {
+    return static_cast<size_t>(kScratchFloats) * sizeof(float);
 }
 
 }  // extern "C"
