@@ -287,17 +287,27 @@ __device__ __forceinline__ float block_reduce(float v) {
     return v;
 }
 
+// Arrival counters of the one-launch folds.  Agent-scope atomics on one
+// 128-byte line serialize (measured: 2048 arrivals on one counter add about
+// 20 us to a 15 us kernel, 64 arrivals on each of 32 counters on separate
+// lines add nothing measurable, the same 32 counters packed on one line add
+// 11 us), so every counter has a line of its own.
+constexpr int kCounterStride = 32;  // uint32 slots per 128-byte line
+
 // Few long rows (a whole-tensor sum, a loss over all logits): each row is
 // split into nseg segments, one 256-thread block a segment, and the partials
 // are folded in the same launch.  Block s reduces segment s (row s / nseg,
 // elements [(s % nseg) * chunk, +chunk)), stores its float32 partial with an
 // agent-coherent store, waits for the store to complete, and counts its
-// arrival in row_counters[row]; the row's last block reads the nseg partials
-// back (agent-coherent loads) and folds them in a fixed order -- thread t
-// takes partials t, t + 256, ... in turn, then the block combines its waves
-// in order -- so the bits do not depend on which block arrived last.  It
-// writes the result and resets the counter for the next launch (device
-// globals start zeroed when the code object loads).
+// arrival on its group's counter (kFoldGroup consecutive segments of the
+// row, so that no counter sees more than kFoldGroup arrivals).  When the row
+// has several groups, each group's last arrival then counts the group on the
+// row's counter.  The row's last arrival reads all nseg partials back with
+// agent-coherent loads and folds them in a fixed order (thread t takes
+// partials t, t + 256, ... in turn, then the block combines its lanes and
+// waves in order), so the bits do not depend on which block came last, and
+// writes the result.  Each counter is reset by its last arrival for the next
+// launch (device globals start zeroed when the code object loads).
 //
 // Ordering: the fold relies on gfx950's memory system, not on a C++ release
 // / acquire pair.  An agent-scope store is issued with sc1 set and written
@@ -306,13 +316,16 @@ __device__ __forceinline__ float block_reduce(float v) {
 // counter's atomic add is issued after it, and the agent-scope loads of the
 // last block (sc1 set) read the coherent level.  An agent-scope release
 // would instead write back this XCD's whole L2 in every block.
-constexpr int64_t kMaxRowCounters = 4096;
-__device__ unsigned int row_counters[kMaxRowCounters];
+constexpr int kFoldGroup = 64;
+constexpr int64_t kMaxFoldGroups = 8192;
+constexpr int64_t kMaxFoldRows = 4096;
+__device__ unsigned int group_counters[kMaxFoldGroups * kCounterStride];
+__device__ unsigned int row_counters[kMaxFoldRows * kCounterStride];
 
 template <typename Tin, int OP, bool VEC>
 __global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
     const typename Elem<Tin>::storage* x, typename Elem<Tin>::storage* out, float* partial,
-    int64_t r, int64_t chunk, int64_t nseg) {
+    int64_t r, int64_t chunk, int64_t nseg, int64_t ngroups) {
     constexpr int N = VEC ? Packet<Tin>::N : 1;
     const int64_t seg = blockIdx.x;
     const int64_t row = seg / nseg, part = seg - row * nseg;
@@ -335,25 +348,45 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
         }
     }
     acc = block_reduce<OP>(acc);
+    // The block's group of segments, and that group's slot among the row's.
+    const int64_t group = part / kFoldGroup;
+    const int64_t first = group * kFoldGroup;
+    const int64_t gsize = nseg - first < kFoldGroup ? nseg - first : kFoldGroup;
+    const int64_t gslot = row * ngroups + group;
     __shared__ bool last;
     if (tid == 0) {
         __hip_atomic_store(&partial[seg], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
-        last = __hip_atomic_fetch_add(&row_counters[row], 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == nseg - 1;
+        bool done = __hip_atomic_fetch_add(&group_counters[gslot * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == gsize - 1;
+        if (done && ngroups > 1) {
+            // The group's last arrival: its partials are all stored; count the
+            // group on the row's counter.
+            __hip_atomic_store(&group_counters[gslot * kCounterStride], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            done = __hip_atomic_fetch_add(&row_counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == ngroups - 1;
+            if (done) {
+                __hip_atomic_store(&row_counters[row * kCounterStride], 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else if (done) {
+            __hip_atomic_store(&group_counters[gslot * kCounterStride], 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        last = done;
     }
     __syncthreads();
     if (!last) return;
+    // Every segment of the row has stored its partial: fold them in order,
+    // thread t taking partials t, t + 256, ...
     const float* q = partial + row * nseg;
     float v = Combine<OP>::identity();
     for (int64_t k = tid; k < nseg; k += kBlock) {
         v = Combine<OP>::apply(v, __hip_atomic_load(q + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
     v = block_reduce<OP>(v);
-    if (tid == 0) {
-        out[row] = Elem<Tin>::store(finish<OP>(v, r, true));
-        __hip_atomic_store(&row_counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (tid == 0) out[row] = Elem<Tin>::store(finish<OP>(v, r, true));
 }
 
 // amax / amin of one thread's N columns over rows row0, row0 + G, ... < end
@@ -413,7 +446,8 @@ __device__ __forceinline__ void cols_keys(float (&acc)[Packet<Tin>::N],
 //
 // FUSE folds the second pass in: the partials are written and read back
 // with agent-coherent accesses; every block counts its arrival in
-// col_counters[o * gridDim.x + blockIdx.x] once its partial stores have
+// col_counters (one 128-byte line per column range o * gridDim.x +
+// blockIdx.x) once its partial stores have
 // completed, and the last of the nchunk blocks of a column range reads the
 // nchunk partials back in chunk order, writes the result, and resets the
 // counter to zero for the next launch.  The counters start at zero (device
@@ -426,7 +460,7 @@ constexpr int col_lanes() {
 }
 
 constexpr int64_t kMaxColCounters = 8192;
-__device__ unsigned int col_counters[kMaxColCounters];
+__device__ unsigned int col_counters[kMaxColCounters * kCounterStride];
 
 template <typename Tin, typename Tout, int OP, bool VEC, bool FUSE>
 __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
@@ -527,7 +561,7 @@ __global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
             // device-scope fence would write back the whole L2 per block.
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            const int64_t slot = o * gridDim.x + blockIdx.x;
+            const int64_t slot = (o * gridDim.x + blockIdx.x) * kCounterStride;
             if (threadIdx.x == 0) {
                 last = __hip_atomic_fetch_add(&col_counters[slot], 1u, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT) == nchunk - 1;
@@ -604,26 +638,29 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     if (inner == 1) {
         const bool vec = r % N == 0 && aligned16(x);
         // Fewer rows than fill the chip, and long ones: split each row into
-        // segments of at least 4096 elements, about eight blocks per CU in
-        // all, and fold the partials in the same launch.
+        // segments of at least 4096 elements, about two blocks per CU in
+        // all, and fold the partials in the same launch.  Measured on a
+        // whole 4096^2 float32 tensor: 11.7 us with two blocks per CU,
+        // against 11.9 (four), 13.0 (eight) and 12.8 (one).
         if (outer < cus * 16 && r >= 8192) {
-            int64_t nseg = (cus * 8 + outer - 1) / outer;
-            const int64_t max_seg = r / 4096;
+            int64_t nseg = (cus * 2 + outer - 1) / outer;
+            const int64_t max_seg = r / 4096;  // >= 2 here
             if (nseg > max_seg) nseg = max_seg;
             int64_t chunk = (r + nseg - 1) / nseg;
             if (vec) chunk = (chunk + N - 1) / N * N;
             nseg = (r + chunk - 1) / chunk;
             if (nseg > 1) {
-                TP_AMD_CHECK(outer <= kMaxRowCounters, "row reduction: ", outer,
-                             " rows exceed the arrival counters");
+                const int64_t ngroups = (nseg + kFoldGroup - 1) / kFoldGroup;
+                TP_AMD_CHECK(outer <= kMaxFoldRows && outer * ngroups <= kMaxFoldGroups,
+                             "row reduction: ", outer, " rows of ", nseg, " segments exceed the arrival counters");
                 const int64_t nsegs = outer * nseg;
                 Partials partial(scratch, nsegs, device);
                 if (vec) {
-                    reduce_rows_fused_kernel<T, OP, true>
-                        <<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(x, out, partial.get(), r, chunk, nseg);
+                    reduce_rows_fused_kernel<T, OP, true><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                        x, out, partial.get(), r, chunk, nseg, ngroups);
                 } else {
-                    reduce_rows_fused_kernel<T, OP, false>
-                        <<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(x, out, partial.get(), r, chunk, nseg);
+                    reduce_rows_fused_kernel<T, OP, false><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                        x, out, partial.get(), r, chunk, nseg, ngroups);
                 }
                 TP_AMD_HIP_CHECK(hipGetLastError());
                 return;
