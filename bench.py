@@ -52,7 +52,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 # for a copy kernel of known size; recorded in
 # profiles/config2_binary2d_hbm_traffic.md.
 DOMINANT_TRAFFIC_BYTES = 536883795
-MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
+MFMA_PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 METRIC = "GEMM TFLOP/s + %MFMA peak; reduce/softmax/eltwise GB/s + %HBM peak"
 N = 8192
 
@@ -358,6 +358,79 @@ def suite_readme(ops, dev, ev, lib):
     graph.capture(step)
     record("mlp_train_step_fp32@graph", med(graph.replay), mode="one recorded-graph replay")
     graph.reset()
+    out["chart_rows"] = suite_chart(ops, dev, ev, med, put, graph_mod)
+    return out
+
+
+def suite_chart(ops, dev, ev, med, put, graph_mod):
+    """The rows of the reference's benchmark chart (docs/images/
+    benchmark-ratio.png) that carry only a ratio against torch_mlu and no
+    time: float16 matmuls and memory-bound operators on 4096^2 (the README's
+    shape for its float32 rows), the float32 -> float16 cast, and the
+    launch-overhead row, add on 16 x 16.  Each gets this GPU's time and its
+    rate against the roofline.  The 16 x 16 add is timed three ways: HIP
+    events around one call, the host's wall time per call over 1000
+    back-to-back asynchronous calls (what an eager loop pays to launch), and
+    the same for replays of a recorded graph of that one add."""
+    out = {}
+    n = 4096
+    e = 2
+
+    def rate(name, ms, nbytes=None, flops=None):
+        row = {"ms": round(ms, 4)}
+        if nbytes is not None:
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            row.update({"GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)})
+        if flops is not None:
+            tf = flops / (ms * 1e-3) / 1e12
+            row.update({"TFLOP/s": round(tf, 1), "mfma_frac": round(tf / MFMA_PEAK_TFLOPS["fp16"], 4)})
+        out[name] = row
+
+    half = lambda shape: ops.to(put(shape), F16)
+    for k in (1024, 4096):
+        a, b, at = half((k, k)), half((k, k)), half((k, k))
+        rate(f"mm_{k}_fp16", med(lambda: ops.mm(a, b)), flops=2 * k ** 3)
+        rate(f"mm_tn_{k}_fp16", med(lambda: ops.mm(at.t(), b)), flops=2 * k ** 3)
+        del a, b, at
+    x, y, row = half((n, n)), half((n, n)), half((n,))
+    nn = n * n
+    rate("add_4096sq_fp16", med(lambda: ops.add(x, y)), 3 * nn * e)
+    z = ops.add(x, y)
+    rate("add__4096sq_fp16", med(lambda: ops.add_(z, y)), 3 * nn * e)
+    rate("add_bcast_4096sq_fp16", med(lambda: ops.add(x, row)), 2 * nn * e)
+    rate("relu_4096sq_fp16", med(lambda: ops.relu(x)), 2 * nn * e)
+    rate("gelu_4096sq_fp16", med(lambda: ops.gelu(x)), 2 * nn * e)
+    rate("exp_4096sq_fp16", med(lambda: ops.exp(x)), 2 * nn * e)
+    rate("softmax_4096sq_fp16", med(lambda: ops.softmax(x, -1)), 2 * nn * e)
+    rate("sum_dim_4096sq_fp16", med(lambda: ops.sum_dim(x, -1)), nn * e)
+    rate("sum_all_4096sq_fp16", med(lambda: ops.sum(x)), nn * e)
+    rate("mul_scalar_4096sq_fp16", med(lambda: ops.mul_scalar(x, 2.5)), 2 * nn * e)
+    x32 = put((n, n))
+    rate("cast_fp32_to_fp16_4096sq", med(lambda: ops.to(x32, F16)), nn * 6)
+    del x, y, z, row, x32
+    a, b = put((16, 16)), put((16, 16))
+    out["add_16x16_fp32"] = {"ms": round(med(lambda: ops.add(a, b)), 4), "timing": "HIP events"}
+    calls = 1000
+
+    def per_call_us(fn):
+        for _ in range(20):
+            fn()
+        ev.lib.tp_amd_synchronize(0)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        ev.lib.tp_amd_synchronize(0)
+        return (time.perf_counter() - t0) / calls * 1e6
+
+    eager_us = per_call_us(lambda: ops.add(a, b))
+    graph = graph_mod.Graph()
+    graph.capture(lambda: ops.add(a, b))
+    replay_us = per_call_us(graph.replay)
+    graph.reset()
+    out["add_16x16_fp32@wall"] = {"eager_us_per_call": round(eager_us, 2),
+                                 "graph_replay_us_per_call": round(replay_us, 2),
+                                 "replay_over_eager": round(replay_us / eager_us, 3),
+                                 "timing": f"host wall time over {calls} back-to-back calls"}
     return out
 
 
@@ -534,6 +607,55 @@ def torch_cpu_config3(cores: int, seconds: float) -> dict:
                       f"X1 [32768, 4096] fp32, {n} pass(es)"}
 
 
+def torch_cpu_config2(cores: int, seconds: float) -> dict:
+    """A calibration line beside the headline's CPU baseline: torch on the
+    host CPU, with the oracle's thread count, running the config-2 step's 26
+    operators on the whole [8192, 8192] operands in float32 and bfloat16
+    storage, GB/s of the same algorithmic bytes; not TensorPlay's CPU path."""
+    torch = _torch_cpu(cores)
+    if torch is None:
+        return {"error": "torch not importable"}
+    g = torch.Generator().manual_seed(0)
+    base = torch.randn(N, N, generator=g)
+    row32, col32 = torch.rand(N, generator=g) * 1.5 + 0.5, torch.rand(N, 1, generator=g) * 1.5 + 0.5
+    grad32 = torch.randn(N, N, generator=g)
+    F = torch.nn.functional
+    prepared = [(tuple(t.to(dt) for t in (base, row32, col32, grad32)), e)
+                for dt, e in ((torch.float32, 4), (torch.bfloat16, 2))]
+    del base, grad32
+
+    def one_pass() -> int:
+        total = 0
+        for (a, row, col, grad), e in prepared:
+            nb = N * N * e
+            for b in (row, col):
+                torch.add(a, b), torch.sub(a, b), torch.mul(a, b), torch.div(a, b)
+                total += 8 * nb
+            w = a.clone()
+            w.add_(row), w.sub_(row), w.mul_(row), w.div_(row)
+            total += 8 * nb
+            a + 2.0, a - 2.0, a * 3.0, a * 0.25
+            total += 8 * nb
+            torch.exp(a), torch.log(a.abs() + 1e-3), torch.sqrt(a.abs()), torch.pow(a, 2)
+            torch.relu(a), F.gelu(a), torch.sigmoid(a)
+            total += 14 * nb
+            y = torch.sigmoid(a)
+            torch.where(a > 0, grad, torch.zeros_like(grad))
+            torch.ops.aten.gelu_backward(grad, a)
+            torch.ops.aten.sigmoid_backward(grad, y)
+            total += 9 * nb
+        return total
+
+    work, n, t0 = 0, 0, time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        work += one_pass()
+        n += 1
+    secs = time.perf_counter() - t0
+    return {"value": float(f"{work / secs / 1e9:.4g}"), "unit": "GB/s", "cores": cores, "kind": "calibration",
+            "seconds": round(secs, 2),
+            "sample": f"torch CPU: the config-2 step's 26 operators on [{N}, {N}] fp32 and bf16, {n} pass(es)"}
+
+
 def cpu_suite(seconds_each: float = 3.0) -> dict:
     """CPU figures beside the suite's sections, in each section's unit: the C
     oracle (float64 arithmetic, OpenMP over the host's cores) on a bounded
@@ -678,6 +800,8 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              through mul + sum, backward, SGD) after one untimed step;
     reduce:  config-3 X1 [32768, 4096], then X2 [4096, 32000]: sum and amax
              over dim -1 and 0, fp32 and bf16, five each;
+    reduce_all: whole-tensor sum and amax of 4096^2 in fp32, fp16 and bf16,
+             then the config-5b loss sum over [8192, 1000] fp32, twenty each;
     softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
              X2 [4096, 32000], fp32 and bf16, five each;
     nn:      the NN-layer suite's shapes, fp32 and bf16, five launches of
@@ -721,6 +845,16 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                         for _ in range(5):
                             fn(x, [dim])
             del x32, x
+    elif what == "reduce_all":
+        g = np.random.default_rng(0)
+        x32 = dev.from_numpy(g.standard_normal((4096, 4096), dtype=np.float32))
+        for x in (x32, ops.to(x32, F16), ops.to(x32, BF16)):
+            for fn in (ops.sum, lambda t: ops.amax(t, [])):
+                for _ in range(20):
+                    fn(x)
+        loss = dev.from_numpy(g.standard_normal((8192, 1000), dtype=np.float32))
+        for _ in range(20):
+            ops.sum(loss)
     elif what == "softmax":
         g = np.random.default_rng(0)
         for shape in ((32768, 4096), (4096, 32000)):
@@ -784,7 +918,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "softmax", "nn", "mlp"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "reduce_all", "softmax", "nn",
+                                         "mlp"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
@@ -864,6 +999,12 @@ def main() -> int:
     if not args.no_cpu:
         log("bench: cpu baseline")
         result["cpu_baseline"] = cpu_baseline()
+        log("bench: torch cpu calibration of the headline")
+        try:
+            result["cpu_baseline"]["torch_cpu_calibration"] = torch_cpu_config2(
+                result["cpu_baseline"]["cores"], 5.0)
+        except Exception as exc:  # noqa: BLE001 - recorded in the JSON line
+            result["cpu_baseline"]["torch_cpu_calibration"] = {"error": repr(exc)}
         if not args.no_suite:
             log("bench: cpu samples of the suite")
             try:
