@@ -1,5 +1,5 @@
-// hipMalloc-backed instance of the caching allocator and its C entry points
-// (replaces tensorplay_mlu/csrc/MLUAllocator.cpp and the allocator part of
+// The hipMalloc-backed block cache and its C entry points (replaces
+// tensorplay_mlu/csrc/MLUAllocator.cpp and the allocator part of
 // Module.cpp:24-37).
 
 #include "allocator.h"
@@ -11,7 +11,7 @@ namespace tp_amd {
 
 namespace {
 
-void* hip_allocate(int device, size_t nbytes, void*) {
+void* hip_acquire(int device, size_t nbytes, void*) {
     DeviceGuard guard(device);
     void* ptr = nullptr;
     const hipError_t status = hipMalloc(&ptr, nbytes);
@@ -28,38 +28,43 @@ void hip_release(int device, void* ptr, void*) {
     (void)hipFree(ptr);
 }
 
-void hip_wait(int device, void*) { synchronize(device); }
+void hip_drain(int device, void*) { synchronize(device); }
 
-using DeviceAllocator = CachingAllocatorCore<kMaxDevices>;
+using DeviceCache = BlockCache<kMaxDevices>;
 
-DeviceAllocator& instance() {
-    // Never destroyed: blocks released during process teardown still come
-    // back here (MLUAllocator.cpp:222-227).
-    static auto* allocator =
-        new DeviceAllocator(AllocatorBackend{&hip_allocate, &hip_release, &hip_wait, nullptr});
-    return *allocator;
+DeviceCache& cache() {
+    // Never destroyed: tensors that die during process teardown still give
+    // their blocks back to it.
+    static auto* c = new DeviceCache(MemoryBackend{&hip_acquire, &hip_release, &hip_drain, nullptr});
+    return *c;
 }
 
 }  // namespace
 
 Block* device_alloc(size_t nbytes, int device) {
     const int index = resolve_device(device);
-    return instance().take<Error>(index, nbytes);
+    return cache().obtain<Error>(index, nbytes);
 }
 
-void device_free(Block* block) { instance().give_back(block); }
+void device_free(Block* block) { cache().recycle(block); }
 
-MemoryStats memory_stats(int device) { return instance().stats(resolve_device(device)); }
+MemoryStats device_memory(int device) { return cache().ledger(resolve_device(device)); }
 
-void reset_peak_memory_stats(int device) { instance().reset_peak(resolve_device(device)); }
+void restart_device_peaks(int device) { cache().restart_peaks(resolve_device(device)); }
 
-void empty_cache() { instance().empty_cache(device_count()); }
+void return_idle_memory() { cache().trim(device_count()); }
 
-void set_capture_holding(bool on) { instance().set_capture_holding(on); }
-void freeze_capture_blocks() { instance().freeze_capture_blocks(); }
-void drop_capture_blocks() { instance().drop_capture_blocks(device_count()); }
-int64_t capture_allocations() { return instance().capture_allocations(); }
-int64_t capture_blocks() { return instance().capture_blocks(); }
+void stamp_recorded_blocks(bool on) {
+    if (on) {
+        cache().begin_stamping();
+    } else {
+        cache().end_stamping();
+    }
+}
+void pin_recorded_blocks() { cache().pin_epoch(); }
+void release_recorded_blocks() { cache().retire_epoch(device_count()); }
+int64_t recorded_grants() { return cache().grants(); }
+int64_t pinned_blocks() { return cache().pinned(); }
 
 }  // namespace tp_amd
 
@@ -73,7 +78,7 @@ extern "C" {
 
 void tp_mlu_memory_stats(int index, int64_t* out) {
     const int status = guarded([&] {
-        const MemoryStats s = memory_stats(index);
+        const MemoryStats s = device_memory(index);
         out[0] = s.allocated;
         out[1] = s.reserved;
         out[2] = s.peak_allocated;
@@ -83,11 +88,11 @@ void tp_mlu_memory_stats(int index, int64_t* out) {
 }
 
 void tp_mlu_reset_peak_memory_stats(int index) {
-    (void)guarded([&] { reset_peak_memory_stats(index); });
+    (void)guarded([&] { restart_device_peaks(index); });
 }
 
 void tp_mlu_empty_cache(void) {
-    (void)guarded([&] { empty_cache(); });
+    (void)guarded([&] { return_idle_memory(); });
 }
 
 int tp_amd_malloc(size_t nbytes, int device, void** ptr, void** ctx) {

@@ -96,12 +96,12 @@ def reset_peak_memory_stats(device=None) -> None:
 
 
 def empty_cache() -> None:
-    """Return cached, unused device memory to the driver."""
+    """Hand every idle cached block back to hipFree (after the device drains)."""
     _library().tp_mlu_empty_cache()
 
 
 def mem_get_info(device=None) -> tuple[int, int]:
-    """(free, total) bytes on the device, as the driver reports them."""
+    """hipMemGetInfo for the device: a (free_bytes, total_bytes) pair."""
     free, total = ctypes.c_size_t(), ctypes.c_size_t()
     check(_library().tp_amd_mem_get_info(_index(device), ctypes.byref(free), ctypes.byref(total)))
     return free.value, total.value

@@ -1,12 +1,12 @@
-// Host-memory instance of the device caching allocator's core, for the CPU
-// tests: the same policy code (allocator_core.h) over malloc with an
-// injectable capacity, so rounding, reuse, statistics and the
-// out-of-memory retry can be checked without a GPU.
+// Host-memory instance of the device block cache, for the CPU tests: the
+// same code (block_cache.h) over malloc with an injectable capacity, so
+// quantization, reuse, statistics, the out-of-memory retry and the
+// recording epochs can be checked without a GPU.
 #include <cstdlib>
 #include <map>
 #include <stdexcept>
 
-#include "../../tensorplay-mlu_amd/csrc/allocator_core.h"
+#include "../../tensorplay-mlu_amd/csrc/block_cache.h"
 
 namespace {
 
@@ -39,7 +39,7 @@ void host_release(int, void* p, void* s) {
 
 void host_wait(int, void* s) { ++static_cast<HostState*>(s)->waits; }
 
-using Core = tp_amd::CachingAllocatorCore<4>;
+using Core = tp_amd::BlockCache<4>;
 Core* g_core = nullptr;
 
 struct Oom : std::runtime_error {
@@ -54,15 +54,15 @@ void shim_reset(size_t cap) {
     delete g_core;
     g_state = HostState{};
     g_state.cap = cap;
-    g_core = new Core(tp_amd::AllocatorBackend{&host_alloc, &host_release, &host_wait, &g_state});
+    g_core = new Core(tp_amd::MemoryBackend{&host_alloc, &host_release, &host_wait, &g_state});
 }
 
-size_t shim_round(size_t n) { return tp_amd::round_size(n); }
+size_t shim_round(size_t n) { return tp_amd::quantize(n); }
 
 // Returns the block (or NULL after an out-of-memory error).
 void* shim_take(int dev, size_t n) {
     try {
-        return g_core->take<Oom>(dev, n);
+        return g_core->obtain<Oom>(dev, n);
     } catch (const Oom&) {
         return nullptr;
     }
@@ -70,26 +70,32 @@ void* shim_take(int dev, size_t n) {
 
 size_t shim_block_size(void* b) { return static_cast<tp_amd::Block*>(b)->size; }
 void* shim_block_ptr(void* b) { return static_cast<tp_amd::Block*>(b)->ptr; }
-void shim_give(void* b) { g_core->give_back(static_cast<tp_amd::Block*>(b)); }
+void shim_give(void* b) { g_core->recycle(static_cast<tp_amd::Block*>(b)); }
 
 void shim_stats(int dev, long long* out) {
-    const tp_amd::MemoryStats s = g_core->stats(dev);
+    const tp_amd::MemoryStats s = g_core->ledger(dev);
     out[0] = s.allocated;
     out[1] = s.reserved;
     out[2] = s.peak_allocated;
     out[3] = s.peak_reserved;
 }
 
-void shim_reset_peak(int dev) { g_core->reset_peak(dev); }
-void shim_empty(void) { g_core->empty_cache(4); }
-size_t shim_cached(int dev) { return g_core->cached_blocks(dev); }
+void shim_reset_peak(int dev) { g_core->restart_peaks(dev); }
+void shim_empty(void) { g_core->trim(4); }
+size_t shim_cached(int dev) { return g_core->idle_count(dev); }
 
-void shim_capture_holding(int on) { g_core->set_capture_holding(on != 0); }
-void shim_freeze(void) { g_core->freeze_capture_blocks(); }
-void shim_drop(void) { g_core->drop_capture_blocks(4); }
+void shim_capture_holding(int on) {
+    if (on) {
+        g_core->begin_stamping();
+    } else {
+        g_core->end_stamping();
+    }
+}
+void shim_freeze(void) { g_core->pin_epoch(); }
+void shim_drop(void) { g_core->retire_epoch(4); }
 void shim_capture_stats(long long* out) {
-    out[0] = g_core->capture_allocations();
-    out[1] = g_core->capture_blocks();
+    out[0] = g_core->grants();
+    out[1] = g_core->pinned();
 }
 
 void shim_counts(long* out) {

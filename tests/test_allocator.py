@@ -1,8 +1,9 @@
-"""The caching allocator's policy (tensorplay_mlu/csrc/MLUAllocator.cpp:37-236)
-on a host-memory backend with an injected capacity: size rounding, best-fit
-reuse within a quarter, statistics and peaks, the release-and-retry-once
-response to out-of-memory, and empty_cache waiting for the device before
-returning blocks.  The same allocator_core.h backs the device allocator."""
+"""The block cache's policy (the reference's MLUAllocator.cpp:42-45, 98-128,
+208-219) on a host-memory backend with an injected capacity: size
+quantization, best-fit reuse within a quarter, statistics and peaks, the
+return-idle-and-retry-once response to out-of-memory, trimming that waits
+for the device before returning blocks, and recording epochs.  The same
+block_cache.h backs the device allocator."""
 
 import ctypes as C
 import os
@@ -55,7 +56,7 @@ def counts(lib):
 @pytest.mark.parametrize("n,want", [(1, 512), (512, 512), (513, 1024), (MiB - 1, MiB),
                                     (MiB, MiB), (MiB + 1, 2 * MiB), (3 * MiB, 4 * MiB),
                                     (4 * MiB, 4 * MiB), (0, 0)])
-def test_round_size(shim, n, want):
+def test_quantize(shim, n, want):
     assert shim.shim_round(n) == want
 
 
@@ -172,3 +173,46 @@ def test_recording_sets_blocks_aside(shim):
     cached = shim.shim_cached(0)
     shim.shim_give(e)
     assert capture_stats(shim)[1] == 0 and shim.shim_cached(0) == cached + 1
+
+
+def test_best_fit_matches_a_brute_force_model(shim):
+    """A random sequence of hand-outs and returns against a plain model of
+    the policy: a request is served by the most recently returned of the
+    smallest idle blocks in [quantized size, quantized size * 5 / 4], else
+    by a new block.  Sizes cluster around the 64-class words of the fine
+    classes' bitmap (32 KiB multiples) and around the 1 MiB edge between
+    fine and 2 MiB classes."""
+    import random
+
+    rng = random.Random(7)
+    shim.shim_reset(1 << 40)
+
+    def quantize(n):
+        step = 512 if n <= MiB else 2 * MiB
+        return (n + step - 1) // step * step
+
+    centres = [32 * 1024 * k for k in (1, 2, 3, 31, 32)] + [MiB, 2 * MiB, 6 * MiB, 40 * MiB]
+    live = []          # (block, ptr, size)
+    idle = []          # model: (size, ptr) in return order
+    for step in range(4000):
+        if live and (rng.random() < 0.45 or len(live) > 60):
+            blk, ptr, size = live.pop(rng.randrange(len(live)))
+            shim.shim_give(blk)
+            idle.append((size, ptr))
+            continue
+        want = max(1, rng.choice(centres) + rng.randint(-3000, 3000))
+        q = quantize(want)
+        fits = [(s, i) for i, (s, p) in enumerate(idle) if q <= s <= q + q // 4]
+        blk = shim.shim_take(0, want)
+        ptr, size = shim.shim_block_ptr(blk), shim.shim_block_size(blk)
+        if fits:
+            best = min(s for s, _ in fits)
+            i = max(i for s, i in fits if s == best)     # most recently returned
+            assert (size, ptr) == idle[i], (step, want, size, idle[i])
+            idle.pop(i)
+        else:
+            assert size == q and all(p != ptr for _, p in idle), (step, want, size)
+        live.append((blk, ptr, size))
+    assert shim.shim_cached(0) == len(idle)
+    for blk, _, _ in live:
+        shim.shim_give(blk)
