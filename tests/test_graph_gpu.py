@@ -1,16 +1,17 @@
 """Recording and replaying device work (tp_mlu_capture_*, the reference's
-GraphCapture.cpp:38-130 and graph.py:38-92) on the GPU: a recorded step
-replays to the same results as the eager step on refilled inputs, several
-times with eager work and synchronisations in between; a step that reads a
-value back cannot be recorded; the allocator sets aside the recording's
-blocks until it is dropped."""
+GraphCapture.cpp:38-130 and graph.py:38-92) on the GPU: on every refilled
+input a recorded step replays to the CPU oracle's results (and to the same
+bits as the eager step, which runs the same kernels), several times with
+eager work and synchronisations in between; a step that reads a value back
+cannot be recorded; the allocator pins the recording's blocks until it is
+discarded."""
 
 import importlib
 
 import numpy as np
 import pytest
 
-from _check import assert_normwise, F32
+from _check import assert_bitexact, assert_normwise, assert_sum, F32
 
 pytestmark = pytest.mark.gpu
 
@@ -32,10 +33,19 @@ def step(ops, x, w, b):
     return z, ops.sum_dim(z, [0])
 
 
-def test_replay_matches_eager(dev, ops, graph_mod, runtime):
+def oracle_step(orc, x, w, b):
+    """The same step on the CPU oracle, one operator at a time (float64
+    inside each, rounded to float32 between them, as the device does)."""
+    y = orc.unary(8, F32, orc.binary(0, F32, orc.gemm(F32, x, w), b))
+    z = orc.softmax(False, F32, y, y.shape[0], y.shape[1], 1)
+    return z, orc.reduce(0, F32, z, 1, z.shape[0], z.shape[1])
+
+
+def test_replay_matches_oracle(dev, ops, orc, graph_mod, runtime):
     rng = np.random.default_rng(3)
-    w = dev.from_numpy(rng.standard_normal((256, 192)).astype(np.float32) / 16)
-    b = dev.from_numpy(rng.standard_normal(192).astype(np.float32))
+    wh = rng.standard_normal((256, 192)).astype(np.float32) / 16
+    bh = rng.standard_normal(192).astype(np.float32)
+    w, b = dev.from_numpy(wh), dev.from_numpy(bh)
     x = dev.from_numpy(rng.standard_normal((128, 256)).astype(np.float32))
     g = graph_mod.Graph()
     try:
@@ -46,9 +56,12 @@ def test_replay_matches_eager(dev, ops, graph_mod, runtime):
             ops.copy_(x, host)                      # refill the recorded input
             g.replay()
             runtime.synchronize()
+            oz, os_ = oracle_step(orc, host, wh, bh)
+            assert_normwise(z.numpy(), oz, F32, 1, f"replay {i}: softmax against the oracle")
+            assert_sum(s.numpy(), os_, F32, f"replay {i}: column sums against the oracle")
             want_z, want_s = step(ops, dev.from_numpy(host), w, b)   # eager, same kernels
-            assert_normwise(z.numpy(), want_z.numpy(), F32, 1, f"replay {i}: softmax")
-            assert_normwise(s.numpy(), want_s.numpy(), F32, 1, f"replay {i}: column sums")
+            assert_bitexact(z.numpy(), want_z.numpy(), f"replay {i}: softmax against eager")
+            assert_bitexact(s.numpy(), want_s.numpy(), f"replay {i}: column sums against eager")
             ops.mul_(x, 0.5)                        # unrelated eager work between replays
             runtime.synchronize()
         allocations, held = g.stats()
