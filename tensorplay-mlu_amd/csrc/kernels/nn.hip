@@ -890,6 +890,90 @@ __global__ __launch_bounds__(kScanThreads) void embedding_scan_kernel(int* count
     if (threadIdx.x == 0) offsets[0] = 0;
 }
 
+// The whole plan in one block when the table has at most kPlanRows rows: the
+// row counts live in LDS (zeroed, then counted with LDS atomics), are scanned
+// in LDS tiles exactly as embedding_scan_kernel scans them in memory --
+// offsets[0 .. V] go to memory, the exclusive prefixes stay in LDS as fill
+// cursors -- and the samples are listed (list[offsets[r] + k] = i, k the
+// arrival order among row r's samples).  One launch instead of five (two
+// zero fills, count, scan, fill), each of which costs the ~4.5 us a launch
+// takes on this GPU whatever its size.
+constexpr int64_t kPlanRows = 32768;
+constexpr int kPlanBatch = 8;
+
+template <typename I>
+__global__ __launch_bounds__(kScanThreads) void embedding_plan_kernel(const void* idx, int64_t n, int64_t V,
+                                                                      int64_t padding_idx, int* offsets,
+                                                                      int* list) {
+    __shared__ int rows[kPlanRows];
+    __shared__ int wave_tot[kScanThreads / kWave];
+    __shared__ int carry_s;
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    for (int64_t r = tid; r < V; r += kScanThreads) rows[r] = 0;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    // Indices are read kPlanBatch at a time before their atomics, so the
+    // loads of a batch are in flight together.
+    auto each_sample = [&](auto&& body) {
+        for (int64_t i0 = tid; i0 < n; i0 += static_cast<int64_t>(kPlanBatch) * kScanThreads) {
+            int64_t r[kPlanBatch];
+#pragma unroll
+            for (int u = 0; u < kPlanBatch; ++u) {
+                const int64_t i = i0 + static_cast<int64_t>(u) * kScanThreads;
+                r[u] = i < n ? index_at<I>(idx, i) : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kPlanBatch; ++u) {
+                if (r[u] >= 0 && r[u] < V && r[u] != padding_idx) body(i0 + static_cast<int64_t>(u) * kScanThreads, r[u]);
+            }
+        }
+    };
+    each_sample([&](int64_t, int64_t r) { atomicAdd(&rows[r], 1); });
+    __syncthreads();
+    constexpr int64_t kRun = static_cast<int64_t>(kWave) * kScanPer;
+    constexpr int64_t kTile = kRun * (kScanThreads / kWave);
+    for (int64_t base = 0; base < V; base += kTile) {
+        const int64_t run0 = base + wave * kRun;
+        int v[kScanPer];
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int64_t r = run0 + k * kWave + lane;
+            v[k] = r < V ? rows[r] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) v[k] = wave_inclusive_scan(v[k]);
+        int total = 0;
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int step_total = __builtin_amdgcn_readlane(v[k], kWave - 1);
+            v[k] += total;
+            total += step_total;
+        }
+        __syncthreads();  // carry_s and wave_tot of the previous tile are read
+        if (lane == 0) wave_tot[wave] = total;
+        __syncthreads();
+        int before = carry_s;
+        for (int w = 0; w < wave; ++w) before += wave_tot[w];
+#pragma unroll
+        for (int k = 0; k < kScanPer; ++k) {
+            const int64_t r = run0 + k * kWave + lane;
+            if (r < V) {
+                const int count = r < V ? rows[r] : 0;
+                offsets[r + 1] = before + v[k];
+                rows[r] = before + v[k] - count;  // exclusive prefix: the row's fill cursor
+            }
+        }
+        __syncthreads();  // everyone has read carry_s
+        if (tid == kScanThreads - 1) carry_s = before + total;
+    }
+    if (tid == 0) offsets[0] = 0;
+    __syncthreads();
+    each_sample([&](int64_t i, int64_t r) {
+        const int pos = atomicAdd(&rows[r], 1);
+        if (pos < n) list[pos] = static_cast<int>(i);  // always true; keeps the write inside `list`
+    });
+}
+
 // list[offsets[r] + k] = i, k the arrival order among row r's samples.
 template <typename I>
 __global__ __launch_bounds__(kBlock) void embedding_fill_kernel(const void* idx, int64_t n, int64_t V,
@@ -1278,22 +1362,31 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
         int* offsets = counts + num_weights;
         int* list = offsets + num_weights + 1;
         int* sorted = list + n;
-        zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(reinterpret_cast<uint32_t*>(counts),
-                                                                              num_weights);
-        if (n > 0) {
+        if (num_weights <= kPlanRows && n <= 65536) {
+            // A small table: the whole plan in one block.
             dispatch_index<float>(index_dtype, [&](auto tag) {
                 using I = decltype(tag);
-                embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(indices, n, num_weights,
-                                                                                   padding_idx, counts);
+                embedding_plan_kernel<I><<<1, kScanThreads, 0, st>>>(indices, n, num_weights, padding_idx,
+                                                                    offsets, list);
             });
-        }
-        embedding_scan_kernel<<<1, kScanThreads, 0, st>>>(counts, offsets, num_weights);
-        if (n > 0) {
-            dispatch_index<float>(index_dtype, [&](auto tag) {
-                using I = decltype(tag);
-                embedding_fill_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
-                    indices, n, num_weights, padding_idx, offsets, counts, list);
-            });
+        } else {
+            zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(
+                reinterpret_cast<uint32_t*>(counts), num_weights);
+            if (n > 0) {
+                dispatch_index<float>(index_dtype, [&](auto tag) {
+                    using I = decltype(tag);
+                    embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(indices, n, num_weights,
+                                                                                       padding_idx, counts);
+                });
+            }
+            embedding_scan_kernel<<<1, kScanThreads, 0, st>>>(counts, offsets, num_weights);
+            if (n > 0) {
+                dispatch_index<float>(index_dtype, [&](auto tag) {
+                    using I = decltype(tag);
+                    embedding_fill_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
+                        indices, n, num_weights, padding_idx, offsets, counts, list);
+                });
+            }
         }
         TP_AMD_DISPATCH_NN(dtype, T, {
             const bool vec = dim % Packet<T>::N == 0 && aligned16(grad) && aligned16(out);

@@ -195,11 +195,13 @@ def test_embedding_dense_backward(dev, ops, orc, dtype, pad, freq):
         assert not orc.to_float(got[pad:pad + 1], dtype).any(), "padding row must stay zero"
 
 
-def test_embedding_dense_backward_large_table(dev, ops, orc):
-    """A 40000-row table with 3000 int32 samples (40 on the last row, padding
-    row 5 with samples of its own): the oracle's gradient, the padding row
-    zero, and the same bits on a second run."""
-    V, D = 40000, 8
+@pytest.mark.parametrize("V", [32768, 40000], ids=["one-block-plan-at-capacity", "multi-kernel-plan"])
+def test_embedding_dense_backward_large_table(dev, ops, orc, V):
+    """A large table with 3000 int32 samples (40 on the last row, padding row
+    5 with samples of its own): the oracle's gradient, the padding row zero,
+    and the same bits on a second run.  32768 rows is the most the one-block
+    plan (row counts in LDS) takes; 40000 rows take the multi-kernel plan."""
+    D = 8
     idx = np.random.default_rng(21).integers(0, V, size=3000).astype(np.int32)
     idx[:40] = V - 1
     idx[40:60] = 5
@@ -209,7 +211,7 @@ def test_embedding_dense_backward_large_table(dev, ops, orc):
     assert_bitexact(ops.embedding_dense_backward(g, i, V, 5, False).numpy(), got, "repeat")
     want = orc.embedding_backward(F32, dy, idx.astype(np.int64), V, 5, False)
     assert got.shape == (V, D)
-    assert_normwise(got, want, F32, float(np.sqrt(40)), "embedding backward V=40000")
+    assert_normwise(got, want, F32, float(np.sqrt(40)), f"embedding backward V={V}")
     assert not got[5].any(), "padding row must stay zero"
 
 
