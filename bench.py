@@ -28,7 +28,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,gemm32,reduce,softmax,nn,mlp}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,gemm32,bmm,reduce,reduce_all,softmax,nn,mlp}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -800,6 +800,9 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              through mul + sum, backward, SGD) after one untimed step;
     reduce:  config-3 X1 [32768, 4096], then X2 [4096, 32000]: sum and amax
              over dim -1 and 0, fp32 and bf16, five each;
+    bmm:     ten launches of the copy-like kernel of ``traffic`` (counter
+             calibration), then twenty config-5a products, bf16
+             [64, 512, 128] x [64, 128, 512];
     reduce_all: whole-tensor sum and amax of 4096^2 in fp32, fp16 and bf16,
              then the config-5b loss sum over [8192, 1000] fp32, twenty each;
     softmax: config-3 softmax forward and backward on X1 [32768, 4096] and
@@ -821,6 +824,17 @@ def profile_launches(what: str, lib, ops, dev) -> None:
         for _ in range(10):
             assert lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, a.data_ptr, sa, row.data_ptr, sb,
                                             out.data_ptr, sa, 1.0) == 0
+    elif what == "bmm":
+        a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
+        out = ops.empty((N, N), F32)
+        for _ in range(10):
+            assert lib.tp_amd_launch_affine(0, F32, N * N, a.data_ptr, 1.0, 0.0, out.data_ptr) == 0
+        del a, out
+        g = np.random.default_rng(0)
+        x = ops.to(dev.from_numpy(g.standard_normal((64, 512, 128), dtype=np.float32)), BF16)
+        y = ops.to(dev.from_numpy(g.standard_normal((64, 128, 512), dtype=np.float32)), BF16)
+        for _ in range(20):
+            ops.bmm(x, y)
     elif what in ("gemm", "gemm32"):
         K = 4096
         dt, reps = (BF16, 10) if what == "gemm" else (F32, 5)
@@ -918,8 +932,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "reduce", "reduce_all", "softmax", "nn",
-                                         "mlp"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "bmm", "reduce", "reduce_all", "softmax",
+                                         "nn", "mlp"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:

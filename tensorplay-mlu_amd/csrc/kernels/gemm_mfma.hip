@@ -755,6 +755,139 @@ void launch(const GemmArgs& p, hipStream_t stream) {
 
 }  // namespace big
 
+// Short products (16-bit, K = 64 or 128: attention-sized bmm) are bound by
+// storing C, not by the MFMAs: bf16 64 x 512 x 128 x 512 reads 16 MB and
+// writes 32 MB.  Here all of K goes into LDS at once (one or two of the big
+// kernel's stages, same layouts), one barrier, and each of the 8 waves then
+// works through its 128 x 64 patch one 32 x 32 tile at a time -- the tile's
+// MFMAs over all of K, then its stores -- so the stores of one tile drain
+// while the MFMAs of the next run, instead of all of C going out after all
+// the products.  The grid is one dimension over batch x tiles, numbered so a
+// batch's tiles (which share A and B panels) stay on one XCD and its L2.
+// Measured on the config-5a bmm against the big kernel on the same box:
+// 12.5 against 15.6 us (rocprof), hipBLASLt 15.0 us.
+namespace smallk {
+
+constexpr int W = 8, WN = 4, TM = 4, TN = 2;
+
+template <typename T, bool A_KMAJOR, bool B_KMAJOR>
+__global__ __launch_bounds__(W * kWave, 1) void gemm_smallk_kernel(GemmArgs p) {
+    using S = typename Elem<T>::storage;
+    using big::BK;
+    using big::STAGE;
+    using big::TILE;
+    __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+    const int grid_n = static_cast<int>(p.n / big::BN);
+    const int tiles = static_cast<int>(p.m / big::BM) * grid_n;
+    const int total = static_cast<int>(gridDim.x);
+    const int pid = total % 8 == 0 ? (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int64_t bi = pid / tiles;
+    const int tile = pid % tiles;
+    const int64_t m0 = static_cast<int64_t>(tile / grid_n) * big::BM;
+    const int64_t n0 = static_cast<int64_t>(tile % grid_n) * big::BN;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int wm = wave / WN, wn = wave % WN;
+    const int l32 = lane % 32, half = lane / 32;
+    const int nk = static_cast<int>(p.k / BK);
+    big::Operand<A_KMAJOR, W, TM> oa;
+    big::Operand<B_KMAJOR, W, TN> ob;
+    oa.init(static_cast<const S*>(p.a) + bi * p.stride_a, p.lda, m0, p.k, wave, lane, wm * TM * 32);
+    ob.init(static_cast<const S*>(p.b) + bi * p.stride_b, p.ldb, n0, p.k, wave, lane, wn * TN * 32);
+    oa.issue(0, lds0, wave);
+    ob.issue(0, lds0 + TILE, wave);
+    if (nk > 1) {
+        oa.issue(1, lds1, wave);
+        ob.issue(1, lds1 + TILE, wave);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    S* C = static_cast<S*>(p.c) + bi * p.stride_c;
+    const S* Cin = static_cast<const S*>(p.cin);
+    // Tiles in a fixed order, fully unrolled, so every fragment offset is
+    // static; the scheduling barrier keeps the next tile's reads out of this
+    // one's stores (otherwise the registers run out and spill).
+#pragma unroll
+    for (int t = 0; t < TM * TN; ++t) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int i = t % TM, j = t / TM;
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+        for (int kt = 0; kt < nk; ++kt) {
+            const char* st = kt == 0 ? lds0 : lds1;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc = Mfma<T>::mma(oa.read(st, i, s), ob.read(st + TILE, j, s), acc);
+        }
+        const int64_t col = n0 + wn * TN * 32 + j * 32 + l32;
+        const int64_t rbase = m0 + wm * TM * 32 + i * 32 + 4 * half;
+        S* cp = C + rbase * p.ldc + col;
+        if (p.beta == 0.0f) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) put_c(&cp[r * p.ldc], Elem<T>::store(p.alpha * acc[4 * g + r]));
+                cp += 8 * p.ldc;
+            }
+        } else if (p.cin_rs == 0) {
+            const float c = p.beta * Elem<T>::load(Cin[bi * p.cin_stride_b + col * p.cin_cs]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) put_c(&cp[r * p.ldc], Elem<T>::store(fmaf(p.alpha, acc[4 * g + r], c)));
+                cp += 8 * p.ldc;
+            }
+        } else {
+            const S* ci = Cin + bi * p.cin_stride_b + rbase * p.cin_rs + col * p.cin_cs;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float c = Elem<T>::load(ci[r * p.cin_rs]);
+                    put_c(&cp[r * p.ldc], Elem<T>::store(fmaf(p.beta, c, p.alpha * acc[4 * g + r])));
+                }
+                cp += 8 * p.ldc;
+                ci += 8 * p.cin_rs;
+            }
+        }
+    }
+}
+
+// K of one or two 64-deep stages, full 256 x 256 tiles, the big kernel's
+// panel rules, and enough tiles to give every CU one.
+template <typename T>
+bool eligible(const GemmArgs& p, int cus) {
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    auto panel_ok = [&](const void* x, int64_t ld, int64_t stride, bool kmajor) {
+        const int64_t bytes = kmajor ? 256 * ld * 2 : p.k * ld * 2;
+        return aligned16(x) && ld % 8 == 0 && stride % 8 == 0 && bytes < (int64_t(1) << 32) &&
+               (kmajor ? ld >= p.k : ld >= 256);
+    };
+    const int64_t tiles = (p.m / big::BM) * (p.n / big::BN) * p.batch;
+    return (p.k == 64 || p.k == 128) && p.m % big::BM == 0 && p.n % big::BN == 0 &&
+           panel_ok(p.a, p.lda, p.stride_a, a_kmajor) && panel_ok(p.b, p.ldb, p.stride_b, b_kmajor) &&
+           tiles >= cus && tiles < (int64_t(1) << 31);
+}
+
+template <typename T>
+void launch(const GemmArgs& p, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((p.m / big::BM) * (p.n / big::BN) * p.batch));
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    if (a_kmajor && b_kmajor) {
+        gemm_smallk_kernel<T, true, true><<<grid, W * kWave, 0, stream>>>(p);
+    } else if (a_kmajor) {
+        gemm_smallk_kernel<T, true, false><<<grid, W * kWave, 0, stream>>>(p);
+    } else if (b_kmajor) {
+        gemm_smallk_kernel<T, false, true><<<grid, W * kWave, 0, stream>>>(p);
+    } else {
+        gemm_smallk_kernel<T, false, false><<<grid, W * kWave, 0, stream>>>(p);
+    }
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace smallk
+
 template <typename T>
 bool mfma_eligible(const GemmArgs& p) {
     constexpr int V = Mfma<T>::V;
@@ -879,6 +1012,10 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
         }
     }
     if constexpr (sizeof(typename Elem<T>::storage) == 2) {
+        if (smallk::eligible<T>(p, cu_count(device))) {
+            smallk::launch<T>(p, stream);
+            return;
+        }
         if (big::eligible<T>(p, cu_count(device))) {
             big::launch<T>(p, stream);
             return;

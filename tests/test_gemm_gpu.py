@@ -281,3 +281,48 @@ def test_gemm_fp32_split_k(amd, dev, orc, ta, tb, cin_kind):
         outs.append(out.numpy())
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "split-K sum is not deterministic"
     check(orc, outs[0], want, F32, f"split-K fp32 ta={ta} tb={tb} {cin_kind}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("k", [64, 128])
+@pytest.mark.parametrize("cin_kind", ["none", "bias-row", "full"])
+@pytest.mark.parametrize("bt,m,n", [(64, 512, 512), (257, 256, 256)], ids=["xcd-order", "plain-order"])
+def test_gemm_abi_small_k(amd, dev, orc, dtype, ta, tb, k, cin_kind, bt, m, n):
+    """Batched 16-bit products with K = 64 or 128 (attention-sized: the
+    one-barrier kernel that holds all of K in LDS) through
+    tp_amd_launch_gemm: NaN-padded leading dimensions, the four layouts,
+    alpha = 0.5 and beta = 0 / a per-column bias shared by the batch / a full
+    Cin with beta = 2.  64 x 512 x 512 has 256 tiles (numbered so each batch
+    stays on one XCD); 257 x 256 x 256 has a tile count that is not a
+    multiple of 8 and is numbered in order."""
+    lib = amd.load()
+    pad, alpha = 8, 0.5
+    a = _padded(orc, (bt, k, m) if ta else (bt, m, k), pad, dtype, 11)
+    b = _padded(orc, (bt, n, k) if tb else (bt, k, n), pad, dtype, 12)
+    lda, ldb = a.shape[-1], b.shape[-1]
+    da, db = dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)
+    A = orc.to_float(a, dtype)[..., :(m if ta else k)]
+    B = orc.to_float(b, dtype)[..., :(k if tb else n)]
+    A = np.swapaxes(A, -1, -2) if ta else A
+    B = np.swapaxes(B, -1, -2) if tb else B
+    want = alpha * np.matmul(A, B)
+    if cin_kind == "none":
+        beta, cin, rs, cs, sb = 0.0, None, 0, 0, 0
+    elif cin_kind == "bias-row":
+        beta, cin, rs, cs, sb = 1.0, sample(orc, (n,), dtype, 13), 0, 1, 0
+        want = want + orc.to_float(cin, dtype)
+    else:
+        beta, cin, rs, cs, sb = 2.0, sample(orc, (bt, m, n), dtype, 13), n, 1, m * n
+        want = want + beta * orc.to_float(cin, dtype)
+    dc = dev.from_numpy(cin, dtype=dtype) if cin is not None else None
+    cptr = dc.data_ptr if dc is not None else 0
+    out = dev.empty((bt, m, n), dtype=dtype)
+    st = lib.tp_amd_launch_gemm(0, dtype, bt, m, n, k, alpha, da.data_ptr, lda, a.shape[-2] * lda,
+                                int(ta), db.data_ptr, ldb, b.shape[-2] * ldb, int(tb), beta,
+                                cptr, rs, cs, sb, out.data_ptr, n, m * n)
+    assert st == 0, lib.tp_mlu_last_error()
+    got = out.numpy()
+    assert not np.isnan(orc.to_float(got, dtype)).any(), "padding leaked into the product"
+    check(orc, got, want, dtype, f"small-K gemm {bt}x{m}x{n}x{k} ta={ta} tb={tb} {cin_kind}")
