@@ -266,6 +266,14 @@ __device__ __forceinline__ uint4 buffer_load16(Rsrc r, uint32_t offset) {
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// The same with the default cache policy: the lines are allocated like any
+// other, so an operand re-read soon (by the next launch over the same
+// tensor, or by the next op) can come from the 256 MB Infinity Cache.
+__device__ __forceinline__ uint4 buffer_load16_cached(Rsrc r, uint32_t offset) {
+    const U32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ void buffer_store16(Rsrc r, uint32_t offset, const uint4& v) {
     const U32x4 d = {v.x, v.y, v.z, v.w};
     __builtin_amdgcn_raw_buffer_store_b128(d, r, offset, 0, kNt);

@@ -116,7 +116,8 @@ __device__ __forceinline__ void load_params(const S_<T>* p, float (&out)[VPT][Pa
 // (WAVES waves each) and walks rows with stride gridDim.x kRows, two rows a
 // step in two register sets: the next row's packets are loaded before this
 // row's reductions, so the loads stay in flight across the barriers.  w and b
-// stay in registers as packets.
+// stay in registers as packets.  Rows load with the default cache policy
+// ([8192, 4096] bf16: 22.5 us, 25.9 us with non-temporal loads).
 template <typename T, int WAVES, int VPT>
 __global__ __launch_bounds__(ln_threads<WAVES>()) void layer_norm_rows_kernel(
     const S_<T>* x, const S_<T>* w, const S_<T>* b, S_<T>* y, float* mean_out, float* rstd_out,
@@ -140,14 +141,14 @@ __global__ __launch_bounds__(ln_threads<WAVES>()) void layer_norm_rows_kernel(
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const uint32_t off = static_cast<uint32_t>(tid + k * kThreads) * 16u;
-            wr[k] = buffer_load16(rw, off);
-            br[k] = buffer_load16(rb, off);
+            wr[k] = buffer_load16_cached(rw, off);
+            br[k] = buffer_load16_cached(rb, off);
         }
     }
     auto fetch = [&](uint4 (&buf)[VPT], int64_t row) {
         const Rsrc r = buffer_over(x + (row < rows ? row : 0) * D, row < rows ? row_bytes : 0);
 #pragma unroll
-        for (int k = 0; k < VPT; ++k) buf[k] = buffer_load16(r, static_cast<uint32_t>(tid + k * kThreads) * 16u);
+        for (int k = 0; k < VPT; ++k) buf[k] = buffer_load16_cached(r, static_cast<uint32_t>(tid + k * kThreads) * 16u);
     };
     auto process = [&](const uint4 (&buf)[VPT], int64_t row) {
         float v[VPT][N];
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(GROUPS * WAVES * kWave) void layer_norm_backward_ro
     {
         const Rsrc rw = buffer_over(w, w != nullptr ? row_bytes : 0);
 #pragma unroll
-        for (int k = 0; k < VPT; ++k) wr[k] = buffer_load16(rw, static_cast<uint32_t>(tid + k * kThreads) * 16u);
+        for (int k = 0; k < VPT; ++k) wr[k] = buffer_load16_cached(rw, static_cast<uint32_t>(tid + k * kThreads) * 16u);
     }
     float pw[VPT][N], pb[VPT][N];
 #pragma unroll
@@ -289,8 +290,8 @@ __global__ __launch_bounds__(GROUPS * WAVES * kWave) void layer_norm_backward_ro
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const uint32_t off = static_cast<uint32_t>(tid + k * kThreads) * 16u;
-            buf.x[k] = buffer_load16(rx, off);
-            buf.d[k] = buffer_load16(rd, off);
+            buf.x[k] = buffer_load16_cached(rx, off);
+            buf.d[k] = buffer_load16_cached(rd, off);
         }
     };
     // xhat and g of packet k (zeros past the row's end).
@@ -733,7 +734,7 @@ __global__ __launch_bounds__(kBlock) void dropout_kernel(const S_<T>* x, S_<T>* 
     keep_bits<N / 4>(t * (N / 4), threshold, k0, k1, off0, off1, m);
     if (vec && e0 + N <= n) {
         float xv[N], o[N];
-        unpack<T>(load_raw_nt(x + e0), xv);
+        unpack<T>(*reinterpret_cast<const uint4*>(x + e0), xv);
 #pragma unroll
         for (int j = 0; j < N; ++j) o[j] = m[j] ? opaque(xv[j] * scale) : 0.0f;
         store_raw_nt(out + e0, pack<T>(o));
