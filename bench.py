@@ -51,7 +51,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 # ``bench.py --profile traffic``), each scaled by what the same counter reads
 # for a copy kernel of known size; recorded in
 # profiles/config2_binary2d_hbm_traffic.md.
-DOMINANT_TRAFFIC_BYTES = 536883795
+DOMINANT_TRAFFIC_BYTES = 536829485
 MFMA_PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 METRIC = "GEMM TFLOP/s + %MFMA peak; reduce/softmax/eltwise GB/s + %HBM peak"
 N = 8192
