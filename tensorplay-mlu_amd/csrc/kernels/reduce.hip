@@ -315,7 +315,11 @@ constexpr int kCounterStride = 32;  // uint32 slots per 128-byte line
 // and s_waitcnt vmcnt(0) returns only once that write is acknowledged; the
 // counter's atomic add is issued after it, and the agent-scope loads of the
 // last block (sc1 set) read the coherent level.  An agent-scope release
-// would instead write back this XCD's whole L2 in every block.
+// would instead write back this XCD's whole L2 in every block.  Other
+// targets are refused at compile time rather than trusted to behave alike.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the one-launch reduction folds rely on gfx950's write-through ordering"
+#endif
 constexpr int kFoldGroup = 64;
 constexpr int64_t kMaxFoldGroups = 8192;
 constexpr int64_t kMaxFoldRows = 4096;
