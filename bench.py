@@ -412,25 +412,50 @@ def suite_chart(ops, dev, ev, med, put, graph_mod):
     out["add_16x16_fp32"] = {"ms": round(med(lambda: ops.add(a, b)), 4), "timing": "HIP events"}
     calls = 1000
 
-    def per_call_us(fn):
+    def per_call_us(fn, n=calls):
         for _ in range(20):
             fn()
         ev.lib.tp_amd_synchronize(0)
         t0 = time.perf_counter()
-        for _ in range(calls):
+        for _ in range(n):
             fn()
         ev.lib.tp_amd_synchronize(0)
-        return (time.perf_counter() - t0) / calls * 1e6
+        return (time.perf_counter() - t0) / n * 1e6
 
-    eager_us = per_call_us(lambda: ops.add(a, b))
-    graph = graph_mod.Graph()
-    graph.capture(lambda: ops.add(a, b))
-    replay_us = per_call_us(graph.replay)
-    graph.reset()
+    def eager_and_replay(fn, n=calls):
+        eager = per_call_us(fn, n)
+        graph = graph_mod.Graph()
+        graph.capture(fn)
+        replay = per_call_us(graph.replay, n)
+        graph.reset()
+        return eager, replay
+
+    eager_us, replay_us = eager_and_replay(lambda: ops.add(a, b))
     out["add_16x16_fp32@wall"] = {"eager_us_per_call": round(eager_us, 2),
                                  "graph_replay_us_per_call": round(replay_us, 2),
                                  "replay_over_eager": round(replay_us / eager_us, 3),
                                  "timing": f"host wall time over {calls} back-to-back calls"}
+
+    # One graph of 100 adds replayed, against the same 100 adds launched
+    # eagerly: what a recorded graph saves per kernel once it holds many.
+    def adds():
+        for _ in range(100):
+            ops.add(a, b)
+
+    eager_us, replay_us = eager_and_replay(adds, 100)
+    out["add_16x16_fp32_x100@wall"] = {"eager_us_per_add": round(eager_us / 100, 2),
+                                      "graph_replay_us_per_add": round(replay_us / 100, 2),
+                                      "replay_over_eager": round(replay_us / eager_us, 3),
+                                      "timing": "host wall time over 100 back-to-back runs of 100 adds"}
+    # Config 1, the README quickstart step on [256, 256]: mm, relu, softmax,
+    # sum and their backward, eager against one recorded-graph replay.
+    wl = importlib.import_module("tensorplay-mlu_amd.workloads")
+    x1, w1 = put((256, 256)), put((256, 256))
+    eager_us, replay_us = eager_and_replay(lambda: wl.quickstart_step(ops, x1, w1), 200)
+    out["config1_quickstart_step@wall"] = {"eager_us": round(eager_us, 2),
+                                          "graph_replay_us": round(replay_us, 2),
+                                          "replay_over_eager": round(replay_us / eager_us, 3),
+                                          "timing": "host wall time over 200 back-to-back steps"}
     return out
 
 
