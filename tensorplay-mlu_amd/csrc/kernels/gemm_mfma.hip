@@ -943,11 +943,11 @@ void launch_config(const GemmArgs& whole, hipStream_t stream) {
 // slice keeps at least 128 of K, a multiple of the kernel's BK = 32.
 constexpr int kFinishBlock = 256;
 
-int splitk_slices(const GemmArgs& p, int cus) {
+int splitk_slices(const GemmArgs& p, int cus, int tile = 128, int min_k = 128) {
     if (p.batch != 1) return 1;
-    const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+    const int64_t tiles = ((p.m + tile - 1) / tile) * ((p.n + tile - 1) / tile);
     int s = 1;
-    while (tiles * s * 2 <= cus && p.k % (s * 2 * 32) == 0 && p.k / (s * 2) >= 128) s *= 2;
+    while (tiles * s * 2 <= cus && p.k % (s * 2 * 32) == 0 && p.k / (s * 2) >= min_k) s *= 2;
     return s;
 }
 
@@ -975,6 +975,7 @@ __global__ __launch_bounds__(kFinishBlock) void splitk_finish_kernel(const float
     }
 }
 
+template <int BM, int BN, int WM, int WN>
 void launch_splitk(const GemmArgs& p, int slices, hipStream_t stream, int device) {
     const int64_t mn = p.m * p.n;
     Workspace ws(static_cast<size_t>(slices * mn) * sizeof(float), device);
@@ -989,7 +990,7 @@ void launch_splitk(const GemmArgs& p, int slices, hipStream_t stream, int device
     q.c = ws.get();
     q.ldc = p.n;
     q.stride_c = mn;
-    launch_config<float, 128, 128, 2, 2>(q, stream);
+    launch_config<float, BM, BN, WM, WN>(q, stream);
     const int64_t blocks = std::min<int64_t>((mn + kFinishBlock - 1) / kFinishBlock, 4 * int64_t{cu_count(device)});
     splitk_finish_kernel<<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
         static_cast<const float*>(ws.get()), slices, p.m, p.n, p.alpha, p.beta,
@@ -1005,9 +1006,24 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     if constexpr (std::is_same<T, float>::value) {
-        const int slices = splitk_slices(p, cu_count(device));
+        const int cus = cu_count(device);
+        const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * p.batch;
+        const int slices = splitk_slices(p, cus);
+        if (p.batch == 1 && tiles * slices * 4 <= cus) {
+            // A product that 128 x 128 tiles, even split over K, leave on
+            // under a quarter of the CUs (config 1's 256^3: 4 tiles, 8
+            // blocks): 64 x 64 tiles of two waves, split down to slices of
+            // 64 of K.
+            const int small = splitk_slices(p, cus, 64, 64);
+            if (small > 1) {
+                launch_splitk<64, 64, 2, 1>(p, small, stream, device);
+            } else {
+                launch_config<float, 64, 64, 2, 1>(p, stream);
+            }
+            return;
+        }
         if (slices > 1) {
-            launch_splitk(p, slices, stream, device);
+            launch_splitk<128, 128, 2, 2>(p, slices, stream, device);
             return;
         }
     }
