@@ -9,7 +9,11 @@
 //     LDS read gives a lane 4 consecutive k that feed 4 back-to-back MFMAs
 //     (lane half h supplies k = 4h + j to MFMA j, for A and B alike, so the
 //     pairing of A and B elements is exact whatever order the sum takes).
-// Three kernels, tried in this order:
+// Kernels, tried in this order:
+//   * 16-bit operands, K of 64 or 128, M and N multiples of 256, at least
+//     one 256 x 256 tile per CU: `smallk` below -- all of K loaded at once,
+//     one barrier, the stores of one 32 x 32 tile overlapping the MFMAs of
+//     the next (attention-sized bmm).
 //   * 16-bit operands, M and N multiples of 256, K of 128, at least one
 //     256 x 256 tile per CU: `big` below -- four waves of 128 x 128 (eight
 //     of 128 x 64 when K <= 256), operand
@@ -19,7 +23,9 @@
 //   * other 16-bit products with a 256 x 256 tile per CU: 256 x 256 with
 //     8 waves (2 x 4, each wave a 128 x 64 patch of 4 x 2 MFMA tiles of
 //     32 x 32).
-//   * everything else: 128 x 128 with 4 waves (2 x 2, each 64 x 64).
+//   * everything else: 128 x 128 with 4 waves (2 x 2, each 64 x 64); a
+//     float32 product too small for those tiles to reach a quarter of the
+//     CUs takes 64 x 64 with 2 waves (each 32 x 64).
 // The last two advance K BK at a time through two LDS stages: while the
 // waves multiply out of one stage, the next K tile is written into the
 // other and the one after is already in flight from global memory, so each
