@@ -24,8 +24,9 @@
 //     8 waves (2 x 4, each wave a 128 x 64 patch of 4 x 2 MFMA tiles of
 //     32 x 32).
 //   * everything else: 128 x 128 with 4 waves (2 x 2, each 64 x 64); a
-//     float32 product too small for those tiles to reach a quarter of the
-//     CUs takes 64 x 64 with 2 waves (each 32 x 64).
+//     product too small for those tiles to reach a quarter of the CUs
+//     (float32: even split over K) takes 64 x 64 with 2 waves (each
+//     32 x 64).
 // The last two advance K BK at a time through two LDS stages: while the
 // waves multiply out of one stage, the next K tile is written into the
 // other and the one after is already in flight from global memory, so each
@@ -1045,6 +1046,13 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
         const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
         if (big_tiles >= cu_count(device)) {
             launch_config<T, 256, 256, 2, 4>(p, stream);
+            return;
+        }
+        // Too few 128 x 128 tiles for a quarter of the CUs (mm 1024^2 has
+        // 64): 64 x 64 tiles of two waves.
+        const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * p.batch;
+        if (tiles * 4 <= cu_count(device)) {
+            launch_config<T, 64, 64, 2, 1>(p, stream);
             return;
         }
     }
