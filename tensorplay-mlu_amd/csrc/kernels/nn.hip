@@ -1092,11 +1092,21 @@ __global__ __launch_bounds__(kBlock) void zero_words_kernel(uint32_t* p, int64_t
 
 // Per sample: loss_i = -w[t_i] x[i, t_i] and its weight w[t_i] (0 and 0 for
 // ignore_index, NaN for a target outside [0, C)).  reduction 0 writes
-// y[i]; otherwise each block writes its (sum loss, sum weight) to part.
+// y[i]; otherwise each block writes its (sum loss, sum weight) to part, and
+// the last block to arrive adds the partials in block order (thread t
+// taking blocks t, t + kBlock, ..., then the block's lanes and waves in
+// order) into y = sum loss (/ sum weight for the mean) and total = sum
+// weight -- one launch.  The arrival order rests on the same gfx950
+// guarantee as the reductions' one-launch folds: agent-scope stores are
+// written through and acknowledged before s_waitcnt vmcnt(0) returns, so
+// they precede the counter's atomic add, and agent-scope loads read the
+// coherent level.  The counter is reset by its last arrival.
+__device__ unsigned int nll_arrivals;
 template <typename T, typename I>
 __global__ __launch_bounds__(kBlock) void nll_kernel(const S_<T>* x, const void* target, const S_<T>* w,
                                                      int64_t n, int64_t C, int64_t ignore_index,
-                                                     int reduction, S_<T>* y, float* part) {
+                                                     int reduction, S_<T>* y, S_<T>* total,
+                                                     float* part) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     float loss = 0.0f, wt = 0.0f;
     if (i < n) {
@@ -1120,6 +1130,7 @@ __global__ __launch_bounds__(kBlock) void nll_kernel(const S_<T>* x, const void*
         s_loss[wave] = loss;
         s_wt[wave] = wt;
     }
+    __shared__ bool last;
     __syncthreads();
     if (threadIdx.x == 0) {
         float a = 0.0f, b = 0.0f;
@@ -1127,24 +1138,37 @@ __global__ __launch_bounds__(kBlock) void nll_kernel(const S_<T>* x, const void*
             a += s_loss[k];
             b += s_wt[k];
         }
-        part[2 * blockIdx.x] = a;
-        part[2 * blockIdx.x + 1] = b;
+        __hip_atomic_store(&part[2 * blockIdx.x], a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part[2 * blockIdx.x + 1], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(&nll_arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+        if (last) __hip_atomic_store(&nll_arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-// The block partials summed in order: y = sum loss (/ sum weight for the
-// mean), total = sum weight.
-template <typename T>
-__global__ void nll_finish_kernel(const float* part, int64_t blocks, int reduction, S_<T>* y,
-                                  S_<T>* total) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    __syncthreads();
+    if (!last) return;
     float a = 0.0f, b = 0.0f;
-    for (int64_t k = 0; k < blocks; ++k) {
-        a += part[2 * k];
-        b += part[2 * k + 1];
+    for (int64_t k = threadIdx.x; k < gridDim.x; k += kBlock) {
+        a += __hip_atomic_load(&part[2 * k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        b += __hip_atomic_load(&part[2 * k + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    y[0] = Elem<T>::store(reduction == 1 ? a / b : a);
-    total[0] = Elem<T>::store(b);
+    a = wave_allreduce(a, Plus{});
+    b = wave_allreduce(b, Plus{});
+    __syncthreads();  // every wave has read s_loss / s_wt above
+    if (lane == 0) {
+        s_loss[wave] = a;
+        s_wt[wave] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ta = 0.0f, tb = 0.0f;
+        for (int k = 0; k < kBlock / kWave; ++k) {
+            ta += s_loss[k];
+            tb += s_wt[k];
+        }
+        y[0] = Elem<T>::store(reduction == 1 ? ta / tb : ta);
+        total[0] = Elem<T>::store(tb);
+    }
 }
 
 // dx[i, c] = (c == t_i) ? -w[t_i] g_i : 0, with g_i = grad[i] (reduction
@@ -1421,13 +1445,9 @@ int tp_amd_launch_nll_loss(int device, int dtype, int64_t n, int64_t classes, co
                 using I = decltype(tag);
                 nll_kernel<T, I><<<blocks, kBlock, 0, st>>>(
                     static_cast<const S_<T>*>(x), target, static_cast<const S_<T>*>(weight), n, classes,
-                    ignore_index, reduction, static_cast<S_<T>*>(y), static_cast<float*>(part.get()));
+                    ignore_index, reduction, static_cast<S_<T>*>(y), static_cast<S_<T>*>(total_weight),
+                    static_cast<float*>(part.get()));
             });
-            if (reduction != 0) {
-                nll_finish_kernel<T><<<1, kWave, 0, st>>>(static_cast<const float*>(part.get()), blocks,
-                                                          reduction, static_cast<S_<T>*>(y),
-                                                          static_cast<S_<T>*>(total_weight));
-            }
         });
         TP_AMD_HIP_CHECK(hipGetLastError());
     });

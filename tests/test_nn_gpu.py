@@ -297,3 +297,22 @@ def test_nll_loss_large_batch(dev, ops, orc):
     got = ops.nll_loss_backward(dev.from_numpy(g), dx_, dt_, None, 1, -100, total).numpy()
     want = orc.nll_loss_backward(F32, g, (n, c), t, total.numpy(), None, 1, -100)
     assert_elementwise(got, want, F32, "large nll backward")
+
+
+@pytest.mark.parametrize("reduction", [1, 2], ids=["mean", "sum"])
+def test_nll_loss_many_blocks_folded_in_one_launch(dev, ops, orc, reduction):
+    """300001 samples: 1172 blocks, more than the last block's 256 threads,
+    so each folding thread adds several partials.  Two calls in a row give
+    the same bits (the arrival counter is reset, the fold order is fixed)."""
+    n, c = 300001, 7
+    x = sample(orc, (n, c), F32, 24)
+    t = np.random.default_rng(25).integers(0, c, size=n).astype(np.int64)
+    t[::11] = 3  # ignore_index
+    dx_, dt_ = dev.from_numpy(x), dev.from_numpy(t)
+    outs = [ops.nll_loss(dx_, dt_, None, reduction, 3) for _ in range(2)]
+    wy, wtotal = orc.nll_loss(F32, x, t, None, reduction, 3)
+    y0, total0 = (v.numpy() for v in outs[0])
+    y1, total1 = (v.numpy() for v in outs[1])
+    assert y0.tobytes() == y1.tobytes() and total0.tobytes() == total1.tobytes()
+    assert_normwise(y0, wy, F32, float(np.sqrt(n)) if reduction == 2 else 1, "loss")
+    assert float(total0) == float(wtotal) == float(np.count_nonzero(t != 3))
