@@ -809,10 +809,12 @@ __global__ __launch_bounds__(kBlock) void embedding_kernel(const S_<T>* weight, 
 }
 
 // The dense gradient gathers instead of scattering: the samples of each
-// table row are listed (count, exclusive scan, fill), then one block per row
-// writes the row once -- the sum of its samples' dy rows in increasing
-// sample order, or zeros -- so the whole table is written exactly once and
-// the result does not depend on timing.
+// table row are listed -- by row ranges in one launch
+// (embedding_plan_range_kernel) or, for batches too large for every block
+// to read, by count, exclusive scan and fill over the whole table -- then
+// one block per row writes the row once: the sum of its samples' dy rows in
+// increasing sample order, or zeros.  The whole table is written exactly
+// once and the result does not depend on timing.
 
 // counts[idx[i]] += 1 for valid, non-padding indices.
 template <typename I>
@@ -891,90 +893,6 @@ __global__ __launch_bounds__(kScanThreads) void embedding_scan_kernel(int* count
     if (threadIdx.x == 0) offsets[0] = 0;
 }
 
-// The whole plan in one block when the table has at most kPlanRows rows: the
-// row counts live in LDS (zeroed, then counted with LDS atomics), are scanned
-// in LDS tiles exactly as embedding_scan_kernel scans them in memory --
-// offsets[0 .. V] go to memory, the exclusive prefixes stay in LDS as fill
-// cursors -- and the samples are listed (list[offsets[r] + k] = i, k the
-// arrival order among row r's samples).  One launch instead of five (two
-// zero fills, count, scan, fill), each of which costs the ~4.5 us a launch
-// takes on this GPU whatever its size.
-constexpr int64_t kPlanRows = 32768;
-constexpr int kPlanBatch = 8;
-
-template <typename I>
-__global__ __launch_bounds__(kScanThreads) void embedding_plan_kernel(const void* idx, int64_t n, int64_t V,
-                                                                      int64_t padding_idx, int* offsets,
-                                                                      int* list) {
-    __shared__ int rows[kPlanRows];
-    __shared__ int wave_tot[kScanThreads / kWave];
-    __shared__ int carry_s;
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    for (int64_t r = tid; r < V; r += kScanThreads) rows[r] = 0;
-    if (tid == 0) carry_s = 0;
-    __syncthreads();
-    // Indices are read kPlanBatch at a time before their atomics, so the
-    // loads of a batch are in flight together.
-    auto each_sample = [&](auto&& body) {
-        for (int64_t i0 = tid; i0 < n; i0 += static_cast<int64_t>(kPlanBatch) * kScanThreads) {
-            int64_t r[kPlanBatch];
-#pragma unroll
-            for (int u = 0; u < kPlanBatch; ++u) {
-                const int64_t i = i0 + static_cast<int64_t>(u) * kScanThreads;
-                r[u] = i < n ? index_at<I>(idx, i) : -1;
-            }
-#pragma unroll
-            for (int u = 0; u < kPlanBatch; ++u) {
-                if (r[u] >= 0 && r[u] < V && r[u] != padding_idx) body(i0 + static_cast<int64_t>(u) * kScanThreads, r[u]);
-            }
-        }
-    };
-    each_sample([&](int64_t, int64_t r) { atomicAdd(&rows[r], 1); });
-    __syncthreads();
-    constexpr int64_t kRun = static_cast<int64_t>(kWave) * kScanPer;
-    constexpr int64_t kTile = kRun * (kScanThreads / kWave);
-    for (int64_t base = 0; base < V; base += kTile) {
-        const int64_t run0 = base + wave * kRun;
-        int v[kScanPer];
-#pragma unroll
-        for (int k = 0; k < kScanPer; ++k) {
-            const int64_t r = run0 + k * kWave + lane;
-            v[k] = r < V ? rows[r] : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < kScanPer; ++k) v[k] = wave_inclusive_scan(v[k]);
-        int total = 0;
-#pragma unroll
-        for (int k = 0; k < kScanPer; ++k) {
-            const int step_total = __builtin_amdgcn_readlane(v[k], kWave - 1);
-            v[k] += total;
-            total += step_total;
-        }
-        __syncthreads();  // carry_s and wave_tot of the previous tile are read
-        if (lane == 0) wave_tot[wave] = total;
-        __syncthreads();
-        int before = carry_s;
-        for (int w = 0; w < wave; ++w) before += wave_tot[w];
-#pragma unroll
-        for (int k = 0; k < kScanPer; ++k) {
-            const int64_t r = run0 + k * kWave + lane;
-            if (r < V) {
-                const int count = r < V ? rows[r] : 0;
-                offsets[r + 1] = before + v[k];
-                rows[r] = before + v[k] - count;  // exclusive prefix: the row's fill cursor
-            }
-        }
-        __syncthreads();  // everyone has read carry_s
-        if (tid == kScanThreads - 1) carry_s = before + total;
-    }
-    if (tid == 0) offsets[0] = 0;
-    __syncthreads();
-    each_sample([&](int64_t i, int64_t r) {
-        const int pos = atomicAdd(&rows[r], 1);
-        if (pos < n) list[pos] = static_cast<int>(i);  // always true; keeps the write inside `list`
-    });
-}
-
 // list[offsets[r] + k] = i, k the arrival order among row r's samples.
 template <typename I>
 __global__ __launch_bounds__(kBlock) void embedding_fill_kernel(const void* idx, int64_t n, int64_t V,
@@ -989,6 +907,53 @@ __global__ __launch_bounds__(kBlock) void embedding_fill_kernel(const void* idx,
     }
 }
 
+// Row `row` of the gradient = the sum of dy's rows entries[0 .. c) in that
+// order (float32, from 0), times 1 / c with scale_grad_by_freq; the block's
+// threads split the columns.
+template <typename T, bool VEC>
+__device__ __forceinline__ void sum_row(const S_<T>* dy, const int* entries, int c, int64_t D,
+                                        int scale_grad_by_freq, S_<T>* row) {
+    constexpr int N = VEC ? Packet<T>::N : 1;
+    const int64_t units = D / N;
+    const float scale = scale_grad_by_freq ? 1.0f / static_cast<float>(c) : 1.0f;
+    for (int64_t q = threadIdx.x; q < units; q += kBlock) {
+        float acc[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[j] = 0.0f;
+        for (int k = 0; k < c; ++k) {
+            const int64_t e = entries[k];
+            if constexpr (VEC) {
+                float v[N];
+                unpack<T>(load_raw_nt(dy + e * D + q * N), v);
+#pragma unroll
+                for (int j = 0; j < N; ++j) acc[j] += v[j];
+            } else {
+                acc[0] += Elem<T>::load(dy[e * D + q]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[j] *= scale;
+        if constexpr (VEC) {
+            store_raw_nt(row + q * N, pack<T>(acc));
+        } else {
+            row[q] = Elem<T>::store(acc[0]);
+        }
+    }
+}
+
+// Row `row` of zeros.
+template <typename T, bool VEC>
+__device__ __forceinline__ void zero_row(int64_t D, S_<T>* row) {
+    constexpr int N = VEC ? Packet<T>::N : 1;
+    for (int64_t q = threadIdx.x; q < D / N; q += kBlock) {
+        if constexpr (VEC) {
+            store_raw_nt(row + q * N, make_uint4(0u, 0u, 0u, 0u));
+        } else {
+            row[q] = Elem<T>::store(0.0f);
+        }
+    }
+}
+
 constexpr int kSortCap = 2048;  // samples of one row ordered in LDS; more go through `sorted`
 
 // Row r of the gradient (one block): the samples listed for r put in
@@ -1000,23 +965,15 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_kernel(const S_<T>* d
                                                                   const int* list, int* sorted, int n_list,
                                                                   int64_t D, int scale_grad_by_freq,
                                                                   S_<T>* out) {
-    constexpr int N = VEC ? Packet<T>::N : 1;
     __shared__ int stage[kSortCap];
     __shared__ int order[kSortCap];
     const int64_t r = blockIdx.x;
     // offsets rise from 0 to at most n; the clamps keep reads inside `list`
     const int off = max(offsets[r], 0);
     const int c = max(0, min(offsets[r + 1], n_list) - off);
-    const int64_t units = D / N;
     S_<T>* row = out + r * D;
     if (c == 0) {
-        for (int64_t q = threadIdx.x; q < units; q += kBlock) {
-            if constexpr (VEC) {
-                store_raw_nt(row + q * N, make_uint4(0u, 0u, 0u, 0u));
-            } else {
-                row[q] = Elem<T>::store(0.0f);
-            }
-        }
+        zero_row<T, VEC>(D, row);
         return;
     }
     const int* entries;
@@ -1050,30 +1007,161 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_kernel(const S_<T>* d
         __syncthreads();
         entries = sorted + off;
     }
-    const float scale = scale_grad_by_freq ? 1.0f / static_cast<float>(c) : 1.0f;
-    for (int64_t q = threadIdx.x; q < units; q += kBlock) {
-        float acc[N];
+    sum_row<T, VEC>(dy, entries, c, D, scale_grad_by_freq, row);
+}
+
+// The plan by row ranges, one launch, for batches whose indices every
+// block can afford to read: block b owns table rows [b R, b R + R) and
+// reads all n indices (from L2 once the first blocks have fetched them).
+// Wave w takes the w-th sixteenth of the samples and counts its rows'
+// samples in wave-private LDS counters; one scan gives each row its start
+// and each (wave, row) its first slot, and a device-wide cursor gives the
+// block its segment of `list`.  A second pass places the samples (from
+// registers when a wave's share is one step of kRangeBatch x 64 samples,
+// else read again): a wave's samples after the previous waves', and inside
+// a 64-sample step the lanes that share a row ranked by lane, so each row's
+// samples are listed in increasing order and the gather needs no sort.
+// starts[r] and counts[r] locate row r's samples.  The last block to finish
+// resets the cursor and the arrival count for the next launch; launches on
+// one device must not overlap (the library runs them on one stream).
+constexpr int kRangeRows = 128;  // most rows a block owns
+constexpr int kRangeThreads = 1024;
+constexpr int kRangeWaves = kRangeThreads / kWave;
+constexpr int kRangeBatch = 8;  // index loads in flight per lane
+constexpr int64_t kRangeReadCap = int64_t{128} << 20;  // bytes of indices all blocks read, each pass
+
+__device__ unsigned int embedding_plan_cursor;    // list entries handed out in this launch
+__device__ unsigned int embedding_plan_arrivals;  // blocks finished in this launch
+
+template <typename I>
+__global__ __launch_bounds__(kRangeThreads) void embedding_plan_range_kernel(const void* idx, int n, int64_t V,
+                                                                      int64_t padding_idx, int rows_per_block,
+                                                                      int* starts, int* counts, int* list) {
+    __shared__ int cursor[kRangeWaves][kRangeRows];
+    __shared__ int first[kRangeRows + 1];
+    __shared__ int base_s;
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+    const int R = static_cast<int>(V - r0 < rows_per_block ? V - r0 : rows_per_block);
+    for (int k = tid; k < kRangeWaves * kRangeRows; k += kRangeThreads) (&cursor[0][0])[k] = 0;
+    __syncthreads();
+    const int64_t share = (static_cast<int64_t>(n) + kRangeWaves - 1) / kRangeWaves;
+    const int64_t s0 = min<int64_t>(n, wave * share), s1 = min<int64_t>(n, s0 + share);
+    // the rows of a step of kRangeBatch x 64 samples relative to r0, -1 for
+    // samples that are not this block's
+    auto step_rows = [&](int64_t base, int (&lr)[kRangeBatch]) {
+        int64_t r[kRangeBatch];
 #pragma unroll
-        for (int j = 0; j < N; ++j) acc[j] = 0.0f;
-        for (int k = 0; k < c; ++k) {
-            const int64_t e = entries[k];
-            if constexpr (VEC) {
-                float v[N];
-                unpack<T>(load_raw_nt(dy + e * D + q * N), v);
-#pragma unroll
-                for (int j = 0; j < N; ++j) acc[j] += v[j];
-            } else {
-                acc[0] += Elem<T>::load(dy[e * D + q]);
-            }
+        for (int u = 0; u < kRangeBatch; ++u) {
+            const int64_t i = base + u * kWave + lane;
+            r[u] = i < s1 ? index_at<I>(idx, i) : -1;
         }
 #pragma unroll
-        for (int j = 0; j < N; ++j) acc[j] *= scale;
-        if constexpr (VEC) {
-            store_raw_nt(row + q * N, pack<T>(acc));
-        } else {
-            row[q] = Elem<T>::store(acc[0]);
+        for (int u = 0; u < kRangeBatch; ++u)
+            lr[u] = r[u] >= r0 && r[u] < r0 + R && r[u] != padding_idx ? static_cast<int>(r[u] - r0) : -1;
+    };
+    int first_step[kRangeBatch];  // kept for the placement pass
+    for (int64_t base = s0; base < s1; base += kRangeBatch * kWave) {
+        int lr[kRangeBatch];
+        step_rows(base, lr);
+#pragma unroll
+        for (int u = 0; u < kRangeBatch; ++u) {
+            if (lr[u] >= 0) atomicAdd(&cursor[wave][lr[u]], 1);
+            if (base == s0) first_step[u] = lr[u];
         }
     }
+    __syncthreads();
+    if (wave == 0) {
+        // first[l] = samples of rows before l; cursor[w][l] = where wave w's
+        // samples of row l start
+        int carry = 0;
+        for (int c0 = 0; c0 < R; c0 += kWave) {
+            const int l = c0 + lane;
+            int c[kRangeWaves], tot = 0;
+#pragma unroll
+            for (int w = 0; w < kRangeWaves; ++w) {
+                c[w] = l < R ? cursor[w][l] : 0;
+                tot += c[w];
+            }
+            const int incl = wave_inclusive_scan(tot);
+            int run = carry + incl - tot;
+            if (l < R) {
+                first[l] = run;
+#pragma unroll
+                for (int w = 0; w < kRangeWaves; ++w) {
+                    cursor[w][l] = run;
+                    run += c[w];
+                }
+            }
+            carry += __builtin_amdgcn_readlane(incl, kWave - 1);
+        }
+        if (lane == 0) {
+            first[R] = carry;
+            base_s = static_cast<int>(__hip_atomic_fetch_add(&embedding_plan_cursor, static_cast<unsigned int>(carry),
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+    }
+    __syncthreads();
+    const int base_b = base_s;
+    for (int l = tid; l < R; l += kRangeThreads) {
+        starts[r0 + l] = base_b + first[l];
+        counts[r0 + l] = first[l + 1] - first[l];
+    }
+    for (int64_t base = s0; base < s1; base += kRangeBatch * kWave) {
+        int lr[kRangeBatch];
+        if (base == s0) {
+#pragma unroll
+            for (int u = 0; u < kRangeBatch; ++u) lr[u] = first_step[u];
+        } else {
+            step_rows(base, lr);
+        }
+#pragma unroll
+        for (int u = 0; u < kRangeBatch; ++u) {
+            uint64_t mask = __builtin_amdgcn_ballot_w64(lr[u] >= 0);
+            int rank = 0, same = 0;
+            while (mask) {
+                const int j = __builtin_ctzll(mask);
+                mask &= mask - 1;
+                const int lj = __builtin_amdgcn_readlane(lr[u], j);
+                same += lj == lr[u];
+                rank += lj == lr[u] && j < lane;
+            }
+            if (lr[u] >= 0) {
+                const int pos = cursor[wave][lr[u]] + rank;
+                // the blocks' segments partition the valid samples: always < n
+                if (base_b + pos < n) list[base_b + pos] = static_cast<int>(base + u * kWave + lane);
+                if (rank == same - 1) cursor[wave][lr[u]] = pos + 1;
+            }
+        }
+    }
+    if (tid == 0) {
+        // This block's cursor add returned before base_s was written, so once
+        // every block has arrived no add of this launch is left.
+        if (__hip_atomic_fetch_add(&embedding_plan_arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            gridDim.x - 1) {
+            __hip_atomic_store(&embedding_plan_cursor, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&embedding_plan_arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Row r of the gradient (one block) from a plan whose rows list their
+// samples in increasing order: list[starts[r] .. starts[r] + counts[r]).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void embedding_gather_ordered_kernel(const S_<T>* dy, const int* starts,
+                                                                          const int* counts, const int* list,
+                                                                          int n_list, int64_t D,
+                                                                          int scale_grad_by_freq, S_<T>* out) {
+    const int64_t r = blockIdx.x;
+    // starts and counts stay inside [0, n]; the clamps keep reads inside `list`
+    const int off = min(max(starts[r], 0), n_list);
+    const int c = max(0, min(counts[r], n_list - off));
+    S_<T>* row = out + r * D;
+    if (c == 0) {
+        zero_row<T, VEC>(D, row);
+        return;
+    }
+    sum_row<T, VEC>(dy, list + off, c, D, scale_grad_by_freq, row);
 }
 
 // A float32 buffer to T (or a plain copy for float32), n elements.
@@ -1380,6 +1468,40 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
         const int index = resolve_device(device);
         DeviceGuard guard(index);
         hipStream_t st = stream(index);
+        // The plan by row ranges (about one block per CU, at most kRangeRows
+        // rows each) when its blocks' index reads stay under kRangeReadCap;
+        // otherwise count, scan and fill over the whole table.
+        const int64_t per_block = std::min<int64_t>(
+            kRangeRows, std::max<int64_t>(1, blocks_for(num_weights, int64_t{cu_count(index)})));
+        const int64_t range_blocks = blocks_for(num_weights, per_block);
+        const int64_t index_bytes = index_dtype == TP_AMD_INT32 ? 4 : 8;
+        if (range_blocks * n * index_bytes <= kRangeReadCap) {
+            // starts [V], counts [V], list [n]
+            Workspace ws(static_cast<size_t>(2 * num_weights + n) * sizeof(int), index);
+            int* starts = static_cast<int*>(ws.get());
+            int* counts = starts + num_weights;
+            int* list = counts + num_weights;
+            dispatch_index<float>(index_dtype, [&](auto tag) {
+                using I = decltype(tag);
+                embedding_plan_range_kernel<I><<<range_blocks, kRangeThreads, 0, st>>>(
+                    indices, static_cast<int>(n), num_weights, padding_idx, static_cast<int>(per_block), starts,
+                    counts, list);
+            });
+            TP_AMD_DISPATCH_NN(dtype, T, {
+                const bool vec = dim % Packet<T>::N == 0 && aligned16(grad) && aligned16(out);
+                if (vec) {
+                    embedding_gather_ordered_kernel<T, true><<<num_weights, kBlock, 0, st>>>(
+                        static_cast<const S_<T>*>(grad), starts, counts, list, static_cast<int>(n), dim,
+                        scale_grad_by_freq, static_cast<S_<T>*>(out));
+                } else {
+                    embedding_gather_ordered_kernel<T, false><<<num_weights, kBlock, 0, st>>>(
+                        static_cast<const S_<T>*>(grad), starts, counts, list, static_cast<int>(n), dim,
+                        scale_grad_by_freq, static_cast<S_<T>*>(out));
+                }
+            });
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            return;
+        }
         // counts / cursors [V], offsets [V + 1], list and sorted [n]
         const size_t words = static_cast<size_t>(2 * num_weights + 1 + 2 * n);
         Workspace ws(words * sizeof(int), index);
@@ -1387,31 +1509,22 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
         int* offsets = counts + num_weights;
         int* list = offsets + num_weights + 1;
         int* sorted = list + n;
-        if (num_weights <= kPlanRows && n <= 65536) {
-            // A small table: the whole plan in one block.
+        zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(
+            reinterpret_cast<uint32_t*>(counts), num_weights);
+        if (n > 0) {
             dispatch_index<float>(index_dtype, [&](auto tag) {
                 using I = decltype(tag);
-                embedding_plan_kernel<I><<<1, kScanThreads, 0, st>>>(indices, n, num_weights, padding_idx,
-                                                                    offsets, list);
+                embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(indices, n, num_weights,
+                                                                                   padding_idx, counts);
             });
-        } else {
-            zero_words_kernel<<<blocks_for(num_weights, kBlock), kBlock, 0, st>>>(
-                reinterpret_cast<uint32_t*>(counts), num_weights);
-            if (n > 0) {
-                dispatch_index<float>(index_dtype, [&](auto tag) {
-                    using I = decltype(tag);
-                    embedding_count_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(indices, n, num_weights,
-                                                                                       padding_idx, counts);
-                });
-            }
-            embedding_scan_kernel<<<1, kScanThreads, 0, st>>>(counts, offsets, num_weights);
-            if (n > 0) {
-                dispatch_index<float>(index_dtype, [&](auto tag) {
-                    using I = decltype(tag);
-                    embedding_fill_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
-                        indices, n, num_weights, padding_idx, offsets, counts, list);
-                });
-            }
+        }
+        embedding_scan_kernel<<<1, kScanThreads, 0, st>>>(counts, offsets, num_weights);
+        if (n > 0) {
+            dispatch_index<float>(index_dtype, [&](auto tag) {
+                using I = decltype(tag);
+                embedding_fill_kernel<I><<<blocks_for(n, kBlock), kBlock, 0, st>>>(
+                    indices, n, num_weights, padding_idx, offsets, counts, list);
+            });
         }
         TP_AMD_DISPATCH_NN(dtype, T, {
             const bool vec = dim % Packet<T>::N == 0 && aligned16(grad) && aligned16(out);

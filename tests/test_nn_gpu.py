@@ -195,24 +195,67 @@ def test_embedding_dense_backward(dev, ops, orc, dtype, pad, freq):
         assert not orc.to_float(got[pad:pad + 1], dtype).any(), "padding row must stay zero"
 
 
-@pytest.mark.parametrize("V", [32768, 40000], ids=["one-block-plan-at-capacity", "multi-kernel-plan"])
-def test_embedding_dense_backward_large_table(dev, ops, orc, V):
-    """A large table with 3000 int32 samples (40 on the last row, padding row
-    5 with samples of its own): the oracle's gradient, the padding row zero,
-    and the same bits on a second run.  32768 rows is the most the one-block
-    plan (row counts in LDS) takes; 40000 rows take the multi-kernel plan."""
+# (V, n, index dtype): 313 blocks of 128 rows read 3000 int32 indices each
+# (3.7 MB, the range plan), or 70000 int64 indices each (175 MB, above the
+# plan's 128 MiB cap: count, scan and fill over the whole table)
+PLAN_CASES = [(40000, 3000, np.int32), (40000, 70000, np.int64)]
+
+
+@pytest.mark.parametrize("V,n,itype", PLAN_CASES, ids=["range-plan", "count-scan-fill"])
+def test_embedding_dense_backward_large_table(dev, ops, orc, V, n, itype):
+    """A large table (40 samples on the last row, padding row 5 with samples
+    of its own): the oracle's gradient, the padding row zero, and the same
+    bits on a second run."""
     D = 8
-    idx = np.random.default_rng(21).integers(0, V, size=3000).astype(np.int32)
+    idx = np.random.default_rng(21).integers(0, V, size=n).astype(itype)
     idx[:40] = V - 1
     idx[40:60] = 5
-    dy = sample(orc, (3000, D), F32, 22)
+    dy = sample(orc, (n, D), F32, 22)
     g, i = dev.from_numpy(dy), dev.from_numpy(idx)
     got = ops.embedding_dense_backward(g, i, V, 5, False).numpy()
     assert_bitexact(ops.embedding_dense_backward(g, i, V, 5, False).numpy(), got, "repeat")
     want = orc.embedding_backward(F32, dy, idx.astype(np.int64), V, 5, False)
     assert got.shape == (V, D)
-    assert_normwise(got, want, F32, float(np.sqrt(40)), f"embedding backward V={V}")
+    counts = np.bincount(idx.astype(np.int64), minlength=V)
+    assert_normwise(got, want, F32, float(np.sqrt(counts.max())), f"embedding backward V={V} n={n}")
     assert not got[5].any(), "padding row must stay zero"
+
+
+def sample_order_sum(orc, dtype, dy, idx, V, pad, freq):
+    """Each row's float32 sum of its samples' dy rows in increasing sample
+    order, starting from 0 (np.add.at adds in index order), times the
+    float32 1 / count with scale_grad_by_freq, stored in `dtype`."""
+    keep = (idx >= 0) & (idx < V) & (idx != pad)
+    acc = np.zeros((V, dy.shape[1]), np.float32)
+    np.add.at(acc, idx[keep].astype(np.int64), orc.to_float(dy, dtype)[keep])
+    if freq:
+        c = np.bincount(idx[keep].astype(np.int64), minlength=V).astype(np.float32)
+        scale = np.float32(1) / np.maximum(c, np.float32(1))
+        acc = acc * scale[:, None]
+    return orc.from_float(acc, dtype)
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("V,n,itype", [(5000, 8192, np.int64), (3000, 12000, np.int32),
+                                       (40000, 70000, np.int64)],
+                         ids=["range-plan-int64", "range-plan-int32", "count-scan-fill"])
+def test_embedding_dense_backward_sums_in_sample_order(dev, ops, orc, dtype, V, n, itype):
+    """Both plans list each row's samples in increasing order and the row is
+    their float32 sum from 0 in that order: bit-exact against that sum, with
+    a 500-sample row, a padding index with samples, out-of-range indices
+    (skipped) and both scalings."""
+    rng = np.random.default_rng(26)
+    D = 64 if n <= 8192 else 8
+    idx = rng.integers(0, V, size=n).astype(itype)
+    idx[rng.permutation(n)[:500]] = 3
+    idx[7:19] = 11
+    idx[100] = V
+    idx[200] = -1
+    dy = sample(orc, (n, D), dtype, 27)
+    g, i = dev.from_numpy(dy, dtype=dtype), dev.from_numpy(idx)
+    for freq in (False, True):
+        got = ops.embedding_dense_backward(g, i, V, 11, freq).numpy()
+        assert_bitexact(got, sample_order_sum(orc, dtype, dy, idx, V, 11, freq), f"freq={freq}")
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
