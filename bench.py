@@ -576,7 +576,12 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 8):
 
 
 def _torch_cpu(cores: int):
-    """torch on the host CPU with the oracle's thread count, or None."""
+    """torch on the host CPU with the oracle's thread count, or None.
+
+    torch stays on the CPU here: imported after the backend, it brings its
+    own copy of the HIP and HSA runtimes into the process (its libraries ask
+    for libamdhip64.so by file name from their own directory), and starting
+    that second runtime on the same GPU is not safe."""
     try:
         import torch
     except ImportError:
