@@ -28,7 +28,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,gemm32,bmm,reduce,reduce_all,softmax,nn,mlp}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,gemm32,linear,bmm,reduce,reduce_all,softmax,nn,mlp}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -879,6 +879,14 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                 assert lib.tp_amd_launch_gemm(0, dt, 1, K, K, K, 1.0, a.data_ptr, K, 0, ta,
                                               b.data_ptr, K, 0, tb, 0.0, None, 0, 0, 0,
                                               c.data_ptr, K, 0) == 0
+    elif what == "linear":
+        # config 4's linear: x [8192, 4096] @ W[11008, 4096]^T + b[11008], bf16
+        g = np.random.default_rng(0)
+        x = ops.to(dev.from_numpy(g.standard_normal((8192, 4096), dtype=np.float32) / 64), BF16)
+        w = ops.to(dev.from_numpy(g.standard_normal((11008, 4096), dtype=np.float32) / 64), BF16)
+        bias = ops.to(dev.from_numpy(g.standard_normal(11008, dtype=np.float32)), BF16)
+        for _ in range(10):
+            ops.linear(x, w, bias)
     elif what == "reduce":
         g = np.random.default_rng(0)
         for shape in ((32768, 4096), (4096, 32000)):
@@ -962,8 +970,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "bmm", "reduce", "reduce_all", "softmax",
-                                         "nn", "mlp"],
+    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "linear", "bmm", "reduce", "reduce_all",
+                                         "softmax", "nn", "mlp"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
