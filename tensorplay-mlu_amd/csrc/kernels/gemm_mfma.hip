@@ -433,7 +433,10 @@ namespace big {
 // Operand tiles move from memory straight into LDS with buffer loads (16
 // bytes a lane, no registers in between).  Each operand tile is 32 KB in one
 // of two layouts, swizzled for gfx950's LDS of 64 four-byte banks (256 bytes
-// a clock: 16 lanes of a ds_read_b128, 32 lanes of an 8-byte read):
+// a clock); both read at zero SQ_LDS_BANK_CONFLICT in every layout, which is
+// what settles a swizzle here (the reasoning below, 16 lanes of a
+// ds_read_b128 and 32 of an 8-byte read a clock, explains these two but is
+// not a complete model of the hardware):
 //   * K-major operand: 256 rows (M or N) of 128 bytes, one row = the tile's
 //     64 k; logical 16-byte chunk c of row r sits at slot c ^ kswz(r).  A
 //     load instruction fills 8 rows; a fragment read (ds_read_b128: 32 rows,
