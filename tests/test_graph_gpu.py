@@ -102,3 +102,73 @@ def test_blocks_set_aside_until_reset(dev, ops, graph_mod, runtime):
     assert np.array_equal(y.numpy(), np.full((1024, 1024), 2.0, np.float32))
     g.reset()                                    # result released, blocks returned
     assert g.stats()[1] == 0
+
+
+def nn_step(ops, t):
+    """NN layers whose kernels keep state on the device or take workspaces:
+    layer norm forward and backward (block partials, then a folding
+    launch), the embedding gradient (the row-range plan's device-wide
+    cursors, reset by the plan's last block), nll_loss forward (the last
+    block folds the partials) and backward, and a whole-tensor sum (one
+    launch, the last block folds)."""
+    D = t["x"].shape[1]
+    y, mean, rstd = ops.native_layer_norm(t["x"], (D,), t["w"], t["b"])
+    dx, dw, db = ops.native_layer_norm_backward(t["dy"], t["x"], (D,), mean, rstd, t["w"], t["b"])
+    de = ops.embedding_dense_backward(t["g"], t["idx"], 3000, 5, False)
+    loss, tw = ops.nll_loss(t["logits"], t["tgt"], None, 1)
+    dl = ops.nll_loss_backward(t["one"], t["logits"], t["tgt"], None, 1, -100, tw)
+    s = ops.sum(t["big"])
+    return y, dx, dw, db, de, loss, dl, s
+
+
+def nn_inputs(rng, i):
+    return {"x": rng.standard_normal((64, 512)).astype(np.float32) * (1 + i),
+            "dy": rng.standard_normal((64, 512)).astype(np.float32),
+            "g": rng.standard_normal((1000, 64)).astype(np.float32),
+            "idx": rng.integers(0, 3000, size=1000).astype(np.int64),
+            "logits": rng.standard_normal((1000, 37)).astype(np.float32),
+            "tgt": rng.integers(0, 37, size=1000).astype(np.int64),
+            "big": rng.standard_normal((1000, 3000)).astype(np.float32)}
+
+
+def test_replay_nn_layers(dev, ops, orc, graph_mod, runtime):
+    """The recorded NN step replays to the eager step's bits on every refilled
+    input, with the same operators run eagerly in between (they use the same
+    device counters and cursors), and its embedding gradient to the float32
+    sum of each row's samples in sample order."""
+    rng = np.random.default_rng(8)
+    wh = rng.standard_normal(512).astype(np.float32)
+    bh = rng.standard_normal(512).astype(np.float32)
+    fixed = {"w": dev.from_numpy(wh), "b": dev.from_numpy(bh),
+             "one": dev.from_numpy(np.array(1.0, np.float32))}
+    t = dict(fixed)
+    t.update({k: dev.from_numpy(v) for k, v in nn_inputs(rng, 0).items()})
+    g = graph_mod.Graph()
+    names = ["y", "dx", "dw", "db", "de", "loss", "dl", "s"]
+    try:
+        outs = g.capture(lambda: nn_step(ops, t))
+        for i in range(3):
+            host = nn_inputs(rng, i + 1)
+            for k, v in host.items():
+                ops.copy_(t[k], v)                  # refill the recorded inputs
+            g.replay()
+            runtime.synchronize()
+            fresh = dict(fixed)
+            fresh.update({k: dev.from_numpy(v) for k, v in host.items()})
+            want = nn_step(ops, fresh)              # eager, same kernels
+            for name, got, w in zip(names, outs, want):
+                assert_bitexact(got.numpy(), w.numpy(), f"replay {i}: {name} against eager")
+            keep = (host["idx"] != 5)
+            acc = np.zeros((3000, 64), np.float32)
+            np.add.at(acc, host["idx"][keep], host["g"][keep])
+            assert_bitexact(outs[4].numpy(), acc, f"replay {i}: embedding gradient in sample order")
+            assert_sum(outs[7].numpy(), np.float32(host["big"].astype(np.float64).sum()), F32,
+                       f"replay {i}: whole-tensor sum against float64")
+            yo, _, _ = orc.layer_norm(F32, host["x"], 512, wh, bh)
+            assert_normwise(outs[0].numpy(), yo, F32, 1, f"replay {i}: layer norm against the oracle")
+            del want, fresh
+            ops.mul_(t["big"], 0.5)                 # unrelated eager work between replays
+            runtime.synchronize()
+    finally:
+        g.reset()
+    assert g.stats()[1] == 0
