@@ -804,6 +804,20 @@ __device__ __forceinline__ int64_t index_at(const void* idx, int64_t i) {
     return static_cast<int64_t>(static_cast<const I*>(idx)[i]);
 }
 
+// Index i through a resource over the index array: 0 past its end, with no
+// branch, so a thread's loads of a batch go out together.
+template <typename I>
+__device__ __forceinline__ int64_t index_load(Rsrc r, int64_t i) {
+    const uint32_t off = static_cast<uint32_t>(i) * static_cast<uint32_t>(sizeof(I));
+    if constexpr (sizeof(I) == 8) {
+        typedef unsigned int U32x2 __attribute__((ext_vector_type(2)));
+        const U32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        return static_cast<int64_t>((static_cast<uint64_t>(v[1]) << 32) | v[0]);
+    } else {
+        return static_cast<int64_t>(static_cast<I>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)));
+    }
+}
+
 // out[i, :] = weight[idx[i], :]; a wave per index.  An index outside
 // [0, V) writes a NaN row.
 template <typename T, typename I, bool VEC>
@@ -1076,12 +1090,15 @@ __global__ __launch_bounds__(kRangeThreads) void embedding_plan_range_kernel(con
     const int64_t s0 = min<int64_t>(n, wave * share), s1 = min<int64_t>(n, s0 + share);
     // the rows of a step of kRangeBatch x 64 samples relative to r0, -1 for
     // samples that are not this block's
+    // The host takes this kernel only while n indices fit a 32-bit offset.
+    const Rsrc ridx = buffer_over(idx, static_cast<uint32_t>(n) * static_cast<uint32_t>(sizeof(I)));
     auto step_rows = [&](int64_t base, int (&lr)[kRangeBatch]) {
         int64_t r[kRangeBatch];
 #pragma unroll
+        for (int u = 0; u < kRangeBatch; ++u) r[u] = index_load<I>(ridx, base + u * kWave + lane);
+#pragma unroll
         for (int u = 0; u < kRangeBatch; ++u) {
-            const int64_t i = base + u * kWave + lane;
-            r[u] = i < s1 ? index_at<I>(idx, i) : -1;
+            if (base + u * kWave + lane >= s1) r[u] = -1;
         }
 #pragma unroll
         for (int u = 0; u < kRangeBatch; ++u)
