@@ -237,13 +237,17 @@ def sample_order_sum(orc, dtype, dy, idx, V, pad, freq):
 
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("V,n,itype", [(5000, 8192, np.int64), (3000, 12000, np.int32),
-                                       (40000, 70000, np.int64)],
-                         ids=["range-plan-int64", "range-plan-int32", "count-scan-fill"])
+                                       (100, 300000, np.int32), (40000, 70000, np.int64)],
+                         ids=["range-plan-int64", "range-plan-int32", "range-plan-13-regions",
+                              "count-scan-fill"])
 def test_embedding_dense_backward_sums_in_sample_order(dev, ops, orc, dtype, V, n, itype):
     """Both plans list each row's samples in increasing order and the row is
     their float32 sum from 0 in that order: bit-exact against that sum, with
     a 500-sample row, a padding index with samples, out-of-range indices
-    (skipped) and both scalings."""
+    (skipped) and both scalings.  The range plan spreads its blocks over 16
+    list regions, fewer when 16 x n entries would pass 2^22: 100 one-row
+    blocks over 300000 int32 indices (120 MB of index reads, under the plan's
+    128 MiB cap) use 13."""
     rng = np.random.default_rng(26)
     D = 64 if n <= 8192 else 8
     idx = rng.integers(0, V, size=n).astype(itype)
