@@ -363,3 +363,44 @@ def test_nll_loss_many_blocks_folded_in_one_launch(dev, ops, orc, reduction):
     assert y0.tobytes() == y1.tobytes() and total0.tobytes() == total1.tobytes()
     assert_normwise(y0, wy, F32, float(np.sqrt(n)) if reduction == 2 else 1, "loss")
     assert float(total0) == float(wtotal) == float(np.count_nonzero(t != 3))
+
+
+# ---- empty inputs ----------------------------------------------------------------
+
+
+def test_empty_inputs_follow_the_reference(dev, ops, orc):
+    """Empty operands take the reference's paths (NNKernels.cpp): layer norm
+    and its backward decline an empty input (:73, :122), as does nll_loss
+    and its backward (nll_native needs numel > 0, :315-320); dropout and
+    its backward return empty results (:181, :228); an embedding lookup of
+    no indices is [0, D] (:252); the gradient of a table from no samples
+    is a zero table, and of an empty table an empty one (:279)."""
+    DeclinedError = tensor_mod().DeclinedError
+    x0 = dev.from_numpy(np.zeros((0, 64), np.float32))
+    with pytest.raises(DeclinedError):
+        ops.native_layer_norm(x0, (64,))
+    st = dev.from_numpy(np.zeros(0, np.float32))
+    with pytest.raises(DeclinedError):
+        ops.native_layer_norm_backward(x0, x0, (64,), st, st)
+    out, mask = ops.native_dropout(x0, 0.5, True, seed=3)
+    assert out.shape == (0, 64) and mask.shape == (0, 64)
+    assert ops.native_dropout_backward(x0, mask, 2.0).shape == (0, 64)
+    w = dev.from_numpy(sample(orc, (10, 8), F32, 40))
+    none = dev.from_numpy(np.zeros(0, np.int64))
+    assert ops.embedding(w, none).shape == (0, 8)
+    g0 = dev.from_numpy(np.zeros((0, 8), np.float32))
+    for V in (10, 3000):   # the range plan with no samples
+        got = ops.embedding_dense_backward(g0, none, V).numpy()
+        assert got.shape == (V, 8) and not got.any()
+    assert ops.embedding_dense_backward(g0, none, 0).shape == (0, 8)
+    with pytest.raises(DeclinedError):
+        ops.nll_loss(dev.from_numpy(np.zeros((0, 5), np.float32)), none, None, 1)
+    with pytest.raises(DeclinedError):
+        ops.nll_loss_backward(dev.from_numpy(np.array(1.0, np.float32)),
+                              dev.from_numpy(np.zeros((0, 5), np.float32)), none, None, 1, -100,
+                              dev.from_numpy(np.array(0.0, np.float32)))
+    # a real call after the empty ones still gives the oracle's answer
+    idx = np.array([1, 4, 4, 9], np.int64)
+    dy = sample(orc, (4, 8), F32, 41)
+    got = ops.embedding_dense_backward(dev.from_numpy(dy), dev.from_numpy(idx), 3000).numpy()
+    assert_bitexact(got, sample_order_sum(orc, F32, dy, idx, 3000, -1, False), "after empty calls")
