@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <numeric>
 #include <set>
 #include <utility>
@@ -398,17 +399,26 @@ void host_to_device(const TensorRef& self, const TensorRef& src) {
     // conversion rules are the same).
     const TensorRef host = expand_to(src, sizes_of(self));
     const int64_t n = numel(self);
-    std::vector<char> dense(static_cast<size_t>(n) * element_size(src.dtype));
-    if (is_contiguous(host)) {
-        std::memcpy(dense.data(), host.data, dense.size());
-    } else {
-        host_gather(dense.data(), host);
+    const size_t nbytes = static_cast<size_t>(n) * element_size(src.dtype);
+    if (is_contiguous(host) && src.dtype == self.dtype && is_contiguous(self)) {
+        // The bytes already lie as the destination wants them.
+        copy_to_device(self.data, host.data, nbytes, self.device);
+        return;
+    }
+    // Otherwise the host bytes go dense (a gather when the source is strided
+    // or broadcast) to a device buffer of the source dtype first.
+    std::unique_ptr<char[]> gathered;
+    const char* dense = static_cast<const char*>(host.data);
+    if (!is_contiguous(host)) {
+        gathered.reset(new char[nbytes]);
+        host_gather(gathered.get(), host);
+        dense = gathered.get();
     }
     Owned staging = empty_on(sizes_of(self), src.dtype, self.device);
-    copy_to_device(staging.ref().data, dense.data(), dense.size(), self.device);
+    copy_to_device(staging.ref().data, dense, nbytes, self.device);
     if (src.dtype == self.dtype) {
         if (is_contiguous(self)) {
-            copy_on_device(self.data, staging.ref().data, dense.size(), self.device);
+            copy_on_device(self.data, staging.ref().data, nbytes, self.device);
         } else {
             strided_copy(self, staging.ref());
         }

@@ -1,10 +1,13 @@
 #include "runtime.h"
 
+#include <algorithm>
 #include <array>
 #include <atomic>
+#include <condition_variable>
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <thread>
 
 #include "tp_amd_runtime.h"
 
@@ -119,11 +122,163 @@ void synchronize(int index) {
     TP_AMD_HIP_CHECK(hipStreamSynchronize(stream(index)));
 }
 
+namespace {
+
+// Host memcpy spread over a few threads: the caller takes the first part,
+// kCopyParts - 1 workers the rest.  The pool is created on first use and
+// never destroyed (its threads would otherwise be torn down during static
+// destruction while idle workers still wait on it).
+constexpr int kCopyParts = 8;
+constexpr size_t kSplitFrom = size_t{256} << 10;  // smaller copies stay on one thread
+
+class CopyPool {
+public:
+    static CopyPool& instance() {
+        static CopyPool* pool = new CopyPool();
+        return *pool;
+    }
+
+    void copy(void* dst, const void* src, size_t n) {
+        if (parts_ == 1 || n < kSplitFrom) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        std::lock_guard<std::mutex> job(job_lock_);  // one copy at a time
+        {
+            std::lock_guard<std::mutex> lock(m_);
+            dst_ = static_cast<char*>(dst);
+            src_ = static_cast<const char*>(src);
+            n_ = n;
+            pending_ = parts_ - 1;
+            ++generation_;
+        }
+        start_.notify_all();
+        copy_part(0);
+        std::unique_lock<std::mutex> lock(m_);
+        finish_.wait(lock, [&] { return pending_ == 0; });
+    }
+
+private:
+    CopyPool() {
+        const unsigned hw = std::thread::hardware_concurrency();
+        parts_ = static_cast<int>(std::min<unsigned>(kCopyParts, hw > 1 ? hw : 1));
+        for (int id = 1; id < parts_; ++id) std::thread([this, id] { work(id); }).detach();
+    }
+
+    // Part `id` of the current copy, in 64-byte multiples.  dst_, src_ and
+    // n_ were written under m_ before the generation moved on, and a worker
+    // reads them after seeing the new generation under m_.
+    void copy_part(int id) const {
+        const size_t per = (n_ / parts_ + 63) & ~size_t{63};
+        const size_t lo = std::min(n_, per * id), hi = std::min(n_, lo + per);
+        if (hi > lo) std::memcpy(dst_ + lo, src_ + lo, hi - lo);
+    }
+
+    void work(int id) {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lock(m_);
+                start_.wait(lock, [&] { return generation_ != seen; });
+                seen = generation_;
+            }
+            copy_part(id);
+            std::lock_guard<std::mutex> lock(m_);
+            if (--pending_ == 0) finish_.notify_one();
+        }
+    }
+
+    int parts_ = 1;
+    std::mutex job_lock_, m_;
+    std::condition_variable start_, finish_;
+    uint64_t generation_ = 0;
+    int pending_ = 0;
+    char* dst_ = nullptr;
+    const char* src_ = nullptr;
+    size_t n_ = 0;
+};
+
+// Large copies between pageable host memory and a device go through
+// kStages pinned chunks of kStageBytes per device (allocated on first use,
+// kept until the process ends): the host copy of one chunk overlaps the DMA
+// of the one before, and an event per chunk says when its buffer is free
+// (to device) or filled (to host).
+constexpr size_t kStageBytes = size_t{4} << 20;
+constexpr int kStages = 4;
+constexpr size_t kStageFrom = size_t{8} << 20;  // smaller copies take the runtime's own path
+
+struct Staging {
+    std::mutex lock;  // one staged copy at a time per device
+    std::array<char*, kStages> buf{};
+    std::array<hipEvent_t, kStages> ready{};
+    bool allocated = false;
+};
+std::array<Staging, kMaxDevices> g_staging;
+
+// The device's staging buffers, allocated on first use; the caller holds
+// st.lock with the device current.
+Staging& staging(int index) {
+    Staging& st = g_staging[index];
+    if (!st.allocated) {
+        for (int b = 0; b < kStages; ++b) {
+            if (st.buf[b] == nullptr) {
+                TP_AMD_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&st.buf[b]), kStageBytes, hipHostMallocDefault));
+            }
+            if (st.ready[b] == nullptr) TP_AMD_HIP_CHECK(hipEventCreateWithFlags(&st.ready[b], hipEventDisableTiming));
+        }
+        st.allocated = true;
+    }
+    return st;
+}
+
+void staged_to_device(char* dst, const char* src, size_t n, hipStream_t s, int index) {
+    Staging& st = g_staging[index];
+    std::lock_guard<std::mutex> lock(st.lock);
+    staging(index);
+    for (size_t off = 0, c = 0; off < n; off += kStageBytes, ++c) {
+        const int b = static_cast<int>(c % kStages);
+        const size_t len = std::min(kStageBytes, n - off);
+        TP_AMD_HIP_CHECK(hipEventSynchronize(st.ready[b]));  // the chunk's last DMA out of it is done
+        CopyPool::instance().copy(st.buf[b], src + off, len);
+        TP_AMD_HIP_CHECK(hipMemcpyAsync(dst + off, st.buf[b], len, hipMemcpyHostToDevice, s));
+        TP_AMD_HIP_CHECK(hipEventRecord(st.ready[b], s));
+    }
+    TP_AMD_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void staged_to_host(char* dst, const char* src, size_t n, hipStream_t s, int index) {
+    Staging& st = g_staging[index];
+    std::lock_guard<std::mutex> lock(st.lock);
+    staging(index);
+    const size_t chunks = (n + kStageBytes - 1) / kStageBytes;
+    auto fill = [&](size_t c) {  // DMA chunk c into its buffer, after the work queued before it
+        const int b = static_cast<int>(c % kStages);
+        const size_t off = c * kStageBytes;
+        TP_AMD_HIP_CHECK(hipMemcpyAsync(st.buf[b], src + off, std::min(kStageBytes, n - off),
+                                        hipMemcpyDeviceToHost, s));
+        TP_AMD_HIP_CHECK(hipEventRecord(st.ready[b], s));
+    };
+    for (size_t c = 0; c < chunks && c < static_cast<size_t>(kStages); ++c) fill(c);
+    for (size_t c = 0; c < chunks; ++c) {
+        const int b = static_cast<int>(c % kStages);
+        const size_t off = c * kStageBytes;
+        TP_AMD_HIP_CHECK(hipEventSynchronize(st.ready[b]));
+        CopyPool::instance().copy(dst + off, st.buf[b], std::min(kStageBytes, n - off));
+        if (c + kStages < chunks) fill(c + kStages);
+    }
+}
+
+}  // namespace
+
 void copy_to_device(void* device_dst, const void* host_src, size_t nbytes, int index) {
     if (nbytes == 0) return;
     DeviceGuard guard(index);
     hipStream_t s = stream(index);
     refuse_while_recording(s, "a host-to-device copy");
+    if (nbytes >= kStageFrom) {
+        staged_to_device(static_cast<char*>(device_dst), static_cast<const char*>(host_src), nbytes, s, index);
+        return;
+    }
     TP_AMD_HIP_CHECK(hipMemcpyAsync(device_dst, host_src, nbytes, hipMemcpyHostToDevice, s));
     TP_AMD_HIP_CHECK(hipStreamSynchronize(s));
 }
@@ -133,6 +288,10 @@ void copy_to_host(void* host_dst, const void* device_src, size_t nbytes, int ind
     DeviceGuard guard(index);
     hipStream_t s = stream(index);
     refuse_while_recording(s, "a device-to-host copy");
+    if (nbytes >= kStageFrom) {
+        staged_to_host(static_cast<char*>(host_dst), static_cast<const char*>(device_src), nbytes, s, index);
+        return;
+    }
     TP_AMD_HIP_CHECK(hipMemcpyAsync(host_dst, device_src, nbytes, hipMemcpyDeviceToHost, s));
     TP_AMD_HIP_CHECK(hipStreamSynchronize(s));
 }

@@ -2,8 +2,10 @@
 (the reference's MLUHooks.cpp:23-44, MLURuntime.cpp:112-129), on the GPU:
 host to device, device to device on one device, and device to host, each
 bit-exact on random bytes; odd sizes and unaligned offsets on both sides;
-64 MiB, the size of the reference README's h2d / d2h rows; a zero-byte copy
-is a no-op."""
+64 MiB, the size of the reference README's h2d / d2h rows; sizes either side
+of 8 MiB, from which host copies go through four pinned 4 MiB chunks, and
+one of 18 chunks (each chunk buffer reused four or five times in each
+direction); a zero-byte copy is a no-op."""
 
 import ctypes as C
 
@@ -20,8 +22,9 @@ def _host_ptr(buf: np.ndarray, offset: int = 0) -> C.c_void_p:
     return C.c_void_p(buf.ctypes.data + offset)
 
 
-@pytest.mark.parametrize("nbytes", [1, 3, 4097, (1 << 20) + 7, 64 << 20],
-                         ids=["1B", "3B", "4097B", "1MiB+7", "64MiB"])
+@pytest.mark.parametrize("nbytes", [1, 3, 4097, (1 << 20) + 7, (8 << 20) - 1, 8 << 20, (8 << 20) + 1,
+                                    64 << 20, (68 << 20) + 5],
+                         ids=["1B", "3B", "4097B", "1MiB+7", "8MiB-1", "8MiB", "8MiB+1", "64MiB", "68MiB+5"])
 @pytest.mark.parametrize("offset", [0, 3], ids=["aligned", "offset3"])
 def test_round_trip_is_bit_exact(amd, dev, ops, nbytes, offset):
     lib = amd.load()
