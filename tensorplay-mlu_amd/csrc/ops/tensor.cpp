@@ -453,9 +453,9 @@ void device_to_host(const TensorRef& self, const TensorRef& src) {
         copy_to_host(self.data, dense.ref().data, nbytes, src.device);
         return;
     }
-    std::vector<char> tmp(nbytes);
-    copy_to_host(tmp.data(), dense.ref().data, nbytes, src.device);
-    host_scatter(self, tmp.data());
+    std::unique_ptr<char[]> tmp(new char[nbytes]);
+    copy_to_host(tmp.get(), dense.ref().data, nbytes, src.device);
+    host_scatter(self, tmp.get());
 }
 
 void device_to_device(const TensorRef& self, const TensorRef& src) {
@@ -463,10 +463,10 @@ void device_to_device(const TensorRef& self, const TensorRef& src) {
         // Between devices: through the host (:199-201).
         const size_t nbytes = static_cast<size_t>(numel(src)) * element_size(src.dtype);
         MaybeOwned packed = contiguous_on_device(src);
-        std::vector<char> tmp(nbytes);
-        copy_to_host(tmp.data(), packed.ref.data, nbytes, src.device);
+        std::unique_ptr<char[]> tmp(new char[nbytes]);
+        copy_to_host(tmp.get(), packed.ref.data, nbytes, src.device);
         TensorRef host = packed.ref;
-        host.data = tmp.data();
+        host.data = tmp.get();
         host.device = -1;
         host.ctx = nullptr;
         host_to_device(self, host);
