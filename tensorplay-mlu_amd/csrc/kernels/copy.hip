@@ -209,12 +209,81 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const typename Src::S* src
     }
 }
 
+// Between 2- and 4-byte types with both buffers 16-byte aligned: a thread
+// converts the elements of one 16-byte packet of the wider type (4 for
+// float32 <-> 16-bit, 8 or 4 when both sides are alike), so each load and
+// store instruction covers one contiguous span (the scalar kernel's lanes
+// move 2 or 4 bytes an access).  Same conversions, same bits.
+template <typename Src, typename Dst>
+constexpr int packed_elems() {
+    return 16 / static_cast<int>(sizeof(typename Src::S) > sizeof(typename Dst::S) ? sizeof(typename Src::S)
+                                                                                     : sizeof(typename Dst::S));
+}
+
+template <int BYTES>
+__device__ __forceinline__ void load_bytes(void* dst, const void* src) {
+    if constexpr (BYTES == 16) {
+        const uint4 v = *static_cast<const uint4*>(src);
+        __builtin_memcpy(dst, &v, 16);
+    } else {
+        const uint2 v = *static_cast<const uint2*>(src);
+        __builtin_memcpy(dst, &v, 8);
+    }
+}
+
+template <int BYTES>
+__device__ __forceinline__ void store_bytes_nt(void* dst, const void* src) {
+    if constexpr (BYTES == 16) {
+        uint4 v;
+        __builtin_memcpy(&v, src, 16);
+        store_raw_nt(dst, v);
+    } else {
+        uint64_t v;
+        __builtin_memcpy(&v, src, 8);
+        __builtin_nontemporal_store(v, static_cast<uint64_t*>(dst));
+    }
+}
+
+template <typename Src, typename Dst>
+__global__ __launch_bounds__(kBlock) void cast_packed_kernel(const typename Src::S* src,
+                                                             typename Dst::S* dst, int64_t groups) {
+    using SS = typename Src::S;
+    using DS = typename Dst::S;
+    constexpr int E = packed_elems<Src, Dst>();
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (g >= groups) return;
+    SS v[E];
+    DS o[E];
+    load_bytes<E * sizeof(SS)>(v, src + g * E);
+#pragma unroll
+    for (int j = 0; j < E; ++j) o[j] = convert<Src, Dst>(v[j]);
+    store_bytes_nt<E * sizeof(DS)>(dst + g * E, o);
+}
+
 template <typename Src, typename Dst>
 void cast_typed(int device, int64_t n, const void* src, void* dst) {
+    using SS = typename Src::S;
+    using DS = typename Dst::S;
+    const SS* s = static_cast<const SS*>(src);
+    DS* d = static_cast<DS*>(dst);
+    constexpr bool kPackable = (sizeof(SS) == 2 || sizeof(SS) == 4) && (sizeof(DS) == 2 || sizeof(DS) == 4) &&
+                               !std::is_same<Src, B1>::value && !std::is_same<Dst, B1>::value;
+    if constexpr (kPackable) {
+        constexpr int E = packed_elems<Src, Dst>();
+        const int64_t groups = n / E;
+        if (groups > 0 && aligned16(src) && aligned16(dst)) {
+            const int64_t blocks = (groups + kBlock - 1) / kBlock;
+            cast_packed_kernel<Src, Dst><<<blocks, kBlock, 0, stream(device)>>>(s, d, groups);
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            s += groups * E;  // the last n % E elements below
+            d += groups * E;
+            n -= groups * E;
+            if (n == 0) return;
+        }
+    }
     const int64_t per_block = static_cast<int64_t>(kBlock) * kPerThread;
     const int64_t blocks = (n + per_block - 1) / per_block;
-    cast_kernel<Src, Dst><<<blocks, kBlock, 0, stream(device)>>>(
-        static_cast<const typename Src::S*>(src), static_cast<typename Dst::S*>(dst), n);
+    cast_kernel<Src, Dst><<<blocks, kBlock, 0, stream(device)>>>(s, d, n);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 

@@ -72,6 +72,22 @@ def test_casts_on_device(dev, ops, orc, src, dst):
     assert_bitexact(got, want, f"cast {src}->{dst}")
 
 
+@pytest.mark.parametrize("src,dst", [(F32, BF16), (F32, F16), (BF16, F32), (F16, F32), (BF16, F16),
+                                     (I32, F32), (F32, I32)])
+def test_casts_packed_and_scalar_paths(dev, ops, orc, src, dst):
+    """Aligned buffers of 2- and 4-byte types convert 8 elements a thread as
+    16-byte packets, the last n % 8 elements and unaligned buffers element by
+    element: the same bits either way.  1003 elements from the start of the
+    buffer (packets and a 3-element tail), and from one element in (a view
+    whose data is 16-byte aligned for neither 2- nor 4-byte elements)."""
+    x = values(orc, (1004,), src)
+    d = dev.from_numpy(x, dtype=src)
+    whole = ops.to(d[0:1003], dst).numpy()
+    shifted = ops.to(d[1:1004], dst).numpy()
+    assert_bitexact(whole, orc.cast(src, dst, x[:1003]), f"cast {src}->{dst}, aligned")
+    assert_bitexact(shifted, orc.cast(src, dst, x[1:]), f"cast {src}->{dst}, unaligned")
+
+
 def test_cast_every_bf16_and_f16_pattern(dev, ops, orc):
     bits = np.arange(1 << 16, dtype=np.uint16)
     for dtype in (BF16, F16):
