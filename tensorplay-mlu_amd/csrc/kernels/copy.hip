@@ -306,21 +306,42 @@ void cast_from(int device, int dst_dtype, int64_t n, const void* src, void* dst)
 
 // ---- strided copy ------------------------------------------------------------
 
-template <typename R>
+// The general case, one element a lane.  The index splits into its
+// coordinates with divisions in I: 32-bit when the element count allows
+// (a 64-bit division is several times the instructions).
+template <typename R, typename I>
 __global__ __launch_bounds__(kBlock) void copy_nd_kernel(NdParams<2> p, R* dst, const R* src,
                                                          int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
          i += stride) {
-        int64_t rem = i, od = 0, os = 0;
+        I rem = static_cast<I>(i);
+        int64_t od = 0, os = 0;
         for (int d = p.ndim - 1; d >= 0; --d) {
-            const int64_t q = rem / p.sizes[d];
-            const int64_t idx = rem - q * p.sizes[d];
+            const I size = static_cast<I>(p.sizes[d]);
+            const I q = rem / size;
+            const int64_t idx = static_cast<int64_t>(rem - q * size);
             od += idx * p.strides[0][d];
             os += idx * p.strides[1][d];
             rem = q;
         }
         dst[od] = src[os];
+    }
+}
+
+// Rows of whole 16-byte packets (a row-padded slice, a narrow): packet c
+// of row r at dst[r * ld_dst + c] and src[r * ld_src + c].  One packet a
+// lane, blockIdx.y walking the rows, no division.
+// (Restrict: without it a store may alias the next load, and the compiler
+// copies the packet as four dependent 4-byte loads and stores.)
+__global__ __launch_bounds__(kBlock) void copy_rows_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                           int64_t rows, int64_t cols, int64_t ld_dst,
+                                                           int64_t ld_src) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const uint4 v = src[r * ld_src + c];
+        store_raw_nt(dst + r * ld_dst + c, v);
     }
 }
 
@@ -367,9 +388,55 @@ void copy_typed(int device, const Layout<2>& l, void* dst, const void* src) {
             return;
         }
     }
-    copy_nd_kernel<R><<<grid_for(n, kBlock * 4, device), kBlock, 0, st>>>(
-        nd_params(l), static_cast<R*>(dst), static_cast<const R*>(src), n);
+    if (n <= int64_t{0xffffffff}) {
+        copy_nd_kernel<R, uint32_t><<<grid_for(n, kBlock * 4, device), kBlock, 0, st>>>(
+            nd_params(l), static_cast<R*>(dst), static_cast<const R*>(src), n);
+    } else {
+        copy_nd_kernel<R, int64_t><<<grid_for(n, kBlock * 4, device), kBlock, 0, st>>>(
+            nd_params(l), static_cast<R*>(dst), static_cast<const R*>(src), n);
+    }
     TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+// The layout in 16-byte elements, when the innermost dimension is
+// contiguous in both operands and the row bytes, every other stride in
+// bytes and both base addresses are multiples of 16; otherwise ndim 0.
+Layout<2> in_packets(const Layout<2>& l, int elem_size, const void* dst, const void* src) {
+    Layout<2> w;
+    const int last = l.ndim - 1;
+    if (l.ndim < 2 || l.strides[0][last] != 1 || l.strides[1][last] != 1 || !aligned16(dst) ||
+        !aligned16(src) || (l.sizes[last] * elem_size) % 16 != 0) {
+        return w;
+    }
+    for (int d = 0; d < last; ++d) {
+        for (int k = 0; k < 2; ++k) {
+            if ((l.strides[k][d] * elem_size) % 16 != 0) return w;
+        }
+    }
+    w.ndim = l.ndim;
+    for (int d = 0; d < last; ++d) {
+        w.sizes[d] = l.sizes[d];
+        for (int k = 0; k < 2; ++k) w.strides[k][d] = l.strides[k][d] * elem_size / 16;
+    }
+    w.sizes[last] = l.sizes[last] * elem_size / 16;
+    w.strides[0][last] = w.strides[1][last] = 1;
+    return w;
+}
+
+void copy_packets(int device, const Layout<2>& w, void* dst, const void* src) {
+    hipStream_t st = stream(device);
+    if (w.ndim == 2) {
+        const int64_t cols = w.sizes[1], rows = w.sizes[0];
+        const dim3 grid(static_cast<unsigned>((cols + kBlock - 1) / kBlock),
+                        static_cast<unsigned>(rows < 65535 ? rows : 65535));
+        if ((cols + kBlock - 1) / kBlock < (int64_t{1} << 31)) {
+            copy_rows_kernel<<<grid, kBlock, 0, st>>>(static_cast<uint4*>(dst), static_cast<const uint4*>(src),
+                                                      rows, cols, w.strides[0][0], w.strides[1][0]);
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            return;
+        }
+    }
+    copy_typed<uint4>(device, w, dst, src);
 }
 
 }  // namespace
@@ -431,6 +498,11 @@ int tp_amd_launch_strided_copy(int device, int elem_size, int ndim, const int64_
         if (n == 0) return;
         if (l.ndim == 0 || (l.ndim == 1 && l.strides[0][0] == 1 && l.strides[1][0] == 1)) {
             copy_on_device(dst, src, static_cast<size_t>(n) * elem_size, index);
+            return;
+        }
+        const Layout<2> w = in_packets(l, elem_size, dst, src);
+        if (w.ndim > 0) {
+            copy_packets(index, w, dst, src);
             return;
         }
         switch (elem_size) {

@@ -53,6 +53,37 @@ def test_strided_copies_both_ways(dev, ops, orc):
     assert_bitexact(dst.numpy(), np.ascontiguousarray(big.T), "into transposed view")
 
 
+@pytest.mark.parametrize("dtype", [U8, BF16, F32, I64], ids=["1B", "2B", "4B", "8B"])
+def test_strided_copies_in_packets(dev, ops, orc, dtype):
+    """Rows whose bytes, strides and base addresses are whole 16-byte packets
+    copy a packet a lane (two dimensions: one kernel walking the rows; more:
+    the general kernel on 16-byte elements); a slice starting off a packet
+    boundary, or rows of a partial packet, keeps the element kernel.  Both
+    directions (a strided source, a strided destination), bit-exact."""
+    es = {U8: 1, BF16: 2, F32: 4, I64: 8}[dtype]
+    per = 16 // es                       # elements in a packet
+    x = values(orc, (96, 8 * per + 40), dtype, 3)
+    d = dev.from_numpy(x, dtype=dtype)
+    cases = [(d[:, 0:4 * per], x[:, 0:4 * per], "row slice"),
+             (d[:, per:5 * per], x[:, per:5 * per], "row slice one packet in"),
+             (d[5:77, 2 * per:8 * per], x[5:77, 2 * per:8 * per], "block"),
+             (d[:, 1:4 * per + 1], x[:, 1:4 * per + 1], "off a packet boundary"),
+             (d[:, 0:4 * per + 1], x[:, 0:4 * per + 1], "partial packet rows")]
+    if es < 16:
+        cases.append((d[:, 3:3 + per], x[:, 3:3 + per], "misaligned packet"))
+    y = values(orc, (4, 30, 6 * per), dtype, 4)
+    dy = dev.from_numpy(y, dtype=dtype)
+    cases.append((dy[:, 3:23, per:5 * per], y[:, 3:23, per:5 * per], "3-D"))
+    for view, want, what in cases:
+        assert_bitexact(ops.contiguous(view).numpy(), np.ascontiguousarray(want), what)
+    # a strided destination: write a block into a row slice of a larger tensor
+    out = dev.from_numpy(np.zeros_like(x), dtype=dtype)
+    ops.copy_(out[:, per:5 * per], dev.from_numpy(np.ascontiguousarray(x[:, 0:4 * per]), dtype=dtype))
+    want = np.zeros_like(x)
+    want[:, per:5 * per] = x[:, 0:4 * per]
+    assert_bitexact(out.numpy(), want, "into a row slice")
+
+
 def test_broadcasting_copy_on_device(dev, ops, orc):
     row = values(orc, (1, 5), F32)
     out = dev.empty((4, 5), F32)
