@@ -350,24 +350,52 @@ __global__ __launch_bounds__(kBlock) void copy_rows_kernel(uint4* __restrict__ d
 // through LDS with one element of padding per row.
 constexpr int kTile = 64;
 
+// A thread's 16 loads go out together before any LDS write (a loop of
+// load, wait, write left one in flight at a time), and full tiles skip the
+// bounds tests.
 template <typename R>
-__global__ __launch_bounds__(kBlock) void transpose_kernel(R* dst, const R* src, int64_t rows,
-                                                           int64_t cols, int64_t ld_dst,
+__global__ __launch_bounds__(kBlock) void transpose_kernel(R* __restrict__ dst, const R* __restrict__ src,
+                                                           int64_t rows, int64_t cols, int64_t ld_dst,
                                                            int64_t ld_src) {
+    constexpr int kStep = kBlock / kTile;  // 4 rows of the tile at a time
+    constexpr int kPer = kTile / kStep;    // 16 elements a thread
     __shared__ R tile[kTile][kTile + 1];
-    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTile;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kTile;
+    // Diagonal tile order: block b takes tile row b % gy and tile column
+    // (b / gy + b % gy) % gx (a bijection), so blocks that run together
+    // read the source's strided rows at different offsets.
+    const int64_t b = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t ty_tile = b % gridDim.y, tx_tile = (b / gridDim.y + ty_tile) % gridDim.x;
+    const int64_t r0 = ty_tile * kTile;
+    const int64_t c0 = tx_tile * kTile;
     const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;  // 64 x 4
+    const bool full = r0 + kTile <= rows && c0 + kTile <= cols;
+    R v[kPer];
     // Read: consecutive threads walk r (the source's unit-stride axis).
-    for (int j = ty; j < kTile; j += kBlock / kTile) {
-        const int64_t r = r0 + tx, c = c0 + j;
-        if (r < rows && c < cols) tile[j][tx] = src[c * ld_src + r];
+    if (full) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) v[k] = src[(c0 + ty + k * kStep) * ld_src + r0 + tx];
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int64_t r = r0 + tx, c = c0 + ty + k * kStep;
+            v[k] = r < rows && c < cols ? src[c * ld_src + r] : R{};
+        }
     }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) tile[ty + k * kStep][tx] = v[k];
     __syncthreads();
     // Write: consecutive threads walk c (the destination's unit-stride axis).
-    for (int j = ty; j < kTile; j += kBlock / kTile) {
-        const int64_t r = r0 + j, c = c0 + tx;
-        if (r < rows && c < cols) dst[r * ld_dst + c] = tile[tx][j];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) v[k] = tile[tx][ty + k * kStep];
+    if (full) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) dst[(r0 + ty + k * kStep) * ld_dst + c0 + tx] = v[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int64_t r = r0 + ty + k * kStep, c = c0 + tx;
+            if (r < rows && c < cols) dst[r * ld_dst + c] = v[k];
+        }
     }
 }
 
