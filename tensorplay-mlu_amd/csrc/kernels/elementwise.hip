@@ -152,8 +152,10 @@ __global__ __launch_bounds__(kBlock) void binary2d_kernel(const typename Elem<T>
 
 // ---- general strided index space --------------------------------------------
 
-// Operand 0 is the output; operands 1..NIN the inputs.
-template <typename T, int NIN, typename F>
+// Operand 0 is the output; operands 1..NIN the inputs.  The index splits
+// into its coordinates with divisions in I: 32-bit when the element count
+// allows (a 64-bit division is several times the instructions).
+template <typename T, int NIN, typename F, typename I>
 __global__ __launch_bounds__(kBlock) void nd_kernel(NdParams<NIN + 1> p,
                                                     typename Elem<T>::storage* out,
                                                     const typename Elem<T>::storage* in0,
@@ -162,12 +164,12 @@ __global__ __launch_bounds__(kBlock) void nd_kernel(NdParams<NIN + 1> p,
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
          i += stride) {
-        int64_t rem = i;
+        I rem = static_cast<I>(i);
         int64_t off[NIN + 1] = {};
         for (int d = p.ndim - 1; d >= 0; --d) {
-            const int64_t size = p.sizes[d];
-            const int64_t q = rem / size;
-            const int64_t idx = rem - q * size;
+            const I size = static_cast<I>(p.sizes[d]);
+            const I q = rem / size;
+            const int64_t idx = static_cast<int64_t>(rem - q * size);
             rem = q;
 #pragma unroll
             for (int k = 0; k <= NIN; ++k) off[k] += idx * p.strides[k][d];
@@ -177,6 +179,56 @@ __global__ __launch_bounds__(kBlock) void nd_kernel(NdParams<NIN + 1> p,
         else v = f(Elem<T>::load(in0[off[1]]), Elem<T>::load(in1[off[2]]));
         out[off[0]] = Elem<T>::store(v);
     }
+}
+
+// Layouts whose innermost dimension is contiguous in the output and in
+// each input, or repeats one input element along it (inner stride 0): the
+// inner dimension moves in 16-byte packets, one a thread, and only the
+// outer coordinates come from divisions (32-bit, once a packet).  `p`
+// holds the outer dimensions; bit k - 1 of `rep` marks input k as
+// repeated.  A broadcast add of [B, M, N] and [B, 1, N] is the common case.
+template <typename T, int NIN, typename F>
+__global__ __launch_bounds__(kBlock) void rows_nd_kernel(NdParams<NIN + 1> p, uint32_t per_row, uint32_t rep,
+                                                         typename Elem<T>::storage* out,
+                                                         const typename Elem<T>::storage* in0,
+                                                         const typename Elem<T>::storage* in1, uint32_t total,
+                                                         F f) {
+    constexpr int N = Packet<T>::N;
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= total) return;
+    uint32_t row = i / per_row;
+    const int64_t e = static_cast<int64_t>(i - row * per_row) * N;
+    int64_t off[NIN + 1] = {};
+    for (int d = p.ndim - 1; d >= 0; --d) {
+        const uint32_t size = static_cast<uint32_t>(p.sizes[d]);
+        const uint32_t q = row / size;
+        const int64_t idx = static_cast<int64_t>(row - q * size);
+        row = q;
+#pragma unroll
+        for (int k = 0; k <= NIN; ++k) off[k] += idx * p.strides[k][d];
+    }
+    auto fetch_in = [&](const typename Elem<T>::storage* x, int64_t o, bool repeated) {
+        Packet<T> v;
+        if (repeated) {
+            const typename Elem<T>::storage s = x[o];
+#pragma unroll
+            for (int j = 0; j < N; ++j) v.v[j] = s;
+        } else {
+            v = load_packet<T>(x + o + e);
+        }
+        return v;
+    };
+    const Packet<T> x0 = fetch_in(in0, off[1], rep & 1u);
+    float y[N];
+    if constexpr (NIN == 1) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) y[j] = f(Elem<T>::load(x0.v[j]));
+    } else {
+        const Packet<T> x1 = fetch_in(in1, off[2], rep & 2u);
+#pragma unroll
+        for (int j = 0; j < N; ++j) y[j] = f(Elem<T>::load(x0.v[j]), Elem<T>::load(x1.v[j]));
+    }
+    store_raw_nt(out + off[0] + e, pack<T>(y));
 }
 
 int64_t flat_grid(int64_t npackets) {
@@ -191,6 +243,57 @@ int64_t nd_grid(int64_t n, int device) {
     return want < cap ? (want > 0 ? want : 1) : cap;
 }
 
+// nd_kernel over the n elements of layout l, with 32-bit index arithmetic
+// when n allows.
+template <typename T, int NIN, typename F>
+void launch_nd(int device, const Layout<NIN + 1>& l, void* out, const void* in0, const void* in1, int64_t n,
+               F f) {
+    using S = typename Elem<T>::storage;
+    if (n <= int64_t{0xffffffff}) {
+        nd_kernel<T, NIN, F, uint32_t><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
+            nd_params(l), static_cast<S*>(out), static_cast<const S*>(in0), static_cast<const S*>(in1), n, f);
+    } else {
+        nd_kernel<T, NIN, F, int64_t><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
+            nd_params(l), static_cast<S*>(out), static_cast<const S*>(in0), static_cast<const S*>(in1), n, f);
+    }
+}
+
+// rows_nd_kernel when the layout allows it (see above); false otherwise.
+template <typename T, int NIN, typename F>
+bool try_rows_nd(int device, const Layout<NIN + 1>& l, void* out, const void* in0, const void* in1, int64_t n,
+                 F f) {
+    using S = typename Elem<T>::storage;
+    constexpr int N = Packet<T>::N;
+    constexpr int64_t kEs = sizeof(S);
+    if (l.ndim < 2 || n > int64_t{0xffffffff}) return false;
+    const int last = l.ndim - 1;
+    const int64_t C = l.sizes[last];
+    if (C % N != 0) return false;
+    const void* base[3] = {out, in0, in1};
+    uint32_t rep = 0;
+    for (int k = 0; k <= NIN; ++k) {
+        if (k > 0 && l.strides[k][last] == 0) {
+            rep |= 1u << (k - 1);
+            continue;
+        }
+        if (l.strides[k][last] != 1 || !aligned16(base[k])) return false;
+        for (int d = 0; d < last; ++d) {
+            if ((l.strides[k][d] * kEs) % 16 != 0) return false;
+        }
+    }
+    Layout<NIN + 1> outer;
+    outer.ndim = last;
+    for (int d = 0; d < last; ++d) {
+        outer.sizes[d] = l.sizes[d];
+        for (int k = 0; k <= NIN; ++k) outer.strides[k][d] = l.strides[k][d];
+    }
+    const uint32_t total = static_cast<uint32_t>(n / N);
+    rows_nd_kernel<T, NIN, F><<<(total + kBlock - 1) / kBlock, kBlock, 0, stream(device)>>>(
+        nd_params(outer), static_cast<uint32_t>(C / N), rep, static_cast<S*>(out), static_cast<const S*>(in0),
+        static_cast<const S*>(in1), total, f);
+    return true;
+}
+
 template <typename T, int NIN, typename F>
 void launch_flat(int device, const void* in0, const void* in1, void* out, int64_t n, F f) {
     using S = typename Elem<T>::storage;
@@ -203,9 +306,7 @@ void launch_flat(int device, const void* in0, const void* in1, void* out, int64_
         l.ndim = 1;
         l.sizes[0] = n;
         for (int k = 0; k <= NIN; ++k) l.strides[k][0] = 1;
-        nd_kernel<T, NIN, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
-            nd_params(l), static_cast<S*>(out), static_cast<const S*>(in0),
-            static_cast<const S*>(in1), n, f);
+        launch_nd<T, NIN, F>(device, l, out, in0, in1, n, f);
     } else {
         flat_kernel<T, NIN, F><<<flat_grid(npackets), kBlock, 0, stream(device)>>>(
             static_cast<const S*>(in0), static_cast<const S*>(in1), static_cast<S*>(out),
@@ -270,7 +371,6 @@ template <typename T, typename F>
 void binary_typed(int device, int ndim, const int64_t* sizes, const void* a,
                   const int64_t* as, const void* b, const int64_t* bs, void* out,
                   const int64_t* os, F f) {
-    using S = typename Elem<T>::storage;
     constexpr int N = Packet<T>::N;
     const int64_t* strides[3] = {os, as, bs};
     const Layout<3> l = coalesce<3>(ndim, sizes, strides);
@@ -294,16 +394,13 @@ void binary_typed(int device, int ndim, const int64_t* sizes, const void* a,
             return;
         }
     }
-    nd_kernel<T, 2, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
-        nd_params(l), static_cast<S*>(out), static_cast<const S*>(a), static_cast<const S*>(b),
-        n, f);
+    if (!try_rows_nd<T, 2, F>(device, l, out, a, b, n, f)) launch_nd<T, 2, F>(device, l, out, a, b, n, f);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
 template <typename T, typename F>
 void unary_typed(int device, int ndim, const int64_t* sizes, const void* x, const int64_t* xs,
                  void* y, F f) {
-    using S = typename Elem<T>::storage;
     int64_t ys[TP_AMD_MAX_DIMS];
     contiguous_strides(ndim, sizes, ys);
     const int64_t* strides[2] = {ys, xs};
@@ -314,8 +411,7 @@ void unary_typed(int device, int ndim, const int64_t* sizes, const void* x, cons
         launch_flat<T, 1, F>(device, x, nullptr, y, n, f);
         return;
     }
-    nd_kernel<T, 1, F><<<nd_grid(n, device), kBlock, 0, stream(device)>>>(
-        nd_params(l), static_cast<S*>(y), static_cast<const S*>(x), nullptr, n, f);
+    if (!try_rows_nd<T, 1, F>(device, l, y, x, nullptr, n, f)) launch_nd<T, 1, F>(device, l, y, x, nullptr, n, f);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 

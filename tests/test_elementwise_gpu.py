@@ -33,7 +33,9 @@ def up(dev, arr, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("sa,sb", [((4, 1, 5), (3, 1)), ((6, 4), (4,)), ((33, 17), (33, 1)),
-                                   ((64, 128), (64, 128)), ((5, 7), ()), ((1, 9), (8, 1))])
+                                   ((64, 128), (64, 128)), ((5, 7), ()), ((1, 9), (8, 1)),
+                                   ((4, 6, 16), (4, 1, 16)), ((3, 1, 24), (1, 5, 24)),
+                                   ((2, 3, 4, 8), (3, 1, 8))])
 def test_binary_with_broadcasting(dev, ops, orc, dtype, sa, sb):
     a = sample(orc, sa, dtype, 0)
     b = sample(orc, sb, dtype, 1, 0.5, 2.0)
@@ -102,6 +104,22 @@ def test_scalar_forms_of_strided_operands(dev, ops, orc, dtype):
     want = orc.affine(dtype, a, 0.5, 0.0)
     want[:, ::2] = orc.affine(dtype, np.ascontiguousarray(want[:, ::2]), 1.0, 1.0)
     assert_elementwise(d.numpy(), want, dtype, "strided in-place", max_ulp=1)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_row_padded_views_in_packets(dev, ops, orc, dtype):
+    """A view whose rows are a prefix of longer rows (inner dimension
+    contiguous, row starts 16-byte aligned) against an operand repeated
+    along the inner dimension, and a unary op on such a view: the inner
+    dimension moves in 16-byte packets.  Bit-exact against the oracle."""
+    big = sample(orc, (4, 6, 32), dtype, 5)
+    col = sample(orc, (4, 6, 1), dtype, 6, 0.5, 2.0)
+    d = up(dev, big, dtype)
+    view = d[:, :, 0:16]
+    a = np.ascontiguousarray(big[:, :, 0:16])
+    assert_bitexact(ops.add(view, up(dev, col, dtype)).numpy(), orc.binary(ADD, dtype, a, col, 1.0), "view + column")
+    assert_bitexact(ops.mul(up(dev, col, dtype), view).numpy(), orc.binary(MUL, dtype, col, a), "column * view")
+    assert_bitexact(ops.relu(view).numpy(), orc.unary(8, dtype, a), "relu of a view")
 
 
 def test_strided_operands(dev, ops, orc):
