@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "device_common.h"
+#include "../allocator.h"
 #include "../runtime.h"
 #include "tp_amd_kernels.h"
 
@@ -560,59 +561,208 @@ __global__ __launch_bounds__(kBlock) void softmax_backward_rows_generic_kernel(
     }
 }
 
-// inner > 1: thread per (outer, inner) position, walking D with stride inner.
-template <typename T>
-__global__ __launch_bounds__(kBlock) void softmax_strided_kernel(
-    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, int64_t outer, int64_t D,
-    int64_t inner, bool log) {
-    const int64_t total = outer * inner;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; t < total;
-         t += stride) {
-        const int64_t o = t / inner, i = t - o * inner;
-        const int64_t base = o * D * inner + i;
-        float m = -INFINITY, s = 0.0f;
-        for (int64_t d = 0; d < D; ++d) {
-            const float v = Elem<T>::load(x[base + d * inner]);
-            if (v == -INFINITY) continue;  // contributes exp(-inf) = 0
-            if (v > m) {
-                s = s * exp_fast(m - v) + 1.0f;
-                m = v;
-            } else {
-                s += exp_fast(v - m);
+// ---- softmax over a dimension that is not the last ---------------------------
+//
+// [outer, D, inner] with inner > 1: a block takes 64 consecutive columns of
+// one outer index (one a lane, so a wave reads 64 neighbours of a row) and
+// one slice of D; its four waves take the slice's rows in turn, eight rows
+// loaded together a lane (rows past the slice are clamped and masked, so
+// the loads carry no branch).  Per column, the forward keeps a running
+// (max, sum of exp) and the backward a running sum; the waves' partials
+// fold through LDS in wave order.  With enough column tiles to fill the GPU
+// there is one slice and one launch (MODE kColFused); otherwise a first
+// launch writes each slice's partials (kColStats) and a second folds them in
+// slice order and writes the output (kColWrite).  The earlier kernel gave
+// each column to one thread, which walked D alone: 2.4 ms for a dim-0
+// softmax of [4096, 4096].
+constexpr int kColWaves = 4;
+constexpr int kColWidth = kWave;  // columns of a block
+constexpr int kColBatch = 8;      // rows loaded together a lane
+constexpr int kColFused = 0, kColStats = 1, kColWrite = 2;
+
+struct ColBlock {
+    int64_t o, c0, d0, d1, sl;
+};
+
+// Block b: column tile b % tiles, slice (b / tiles) % slices, outer index
+// b / (tiles * slices).
+__device__ __forceinline__ ColBlock col_block(int64_t tiles, int64_t slices, int64_t D, int64_t dslice) {
+    ColBlock cb;
+    int64_t b = blockIdx.x;
+    cb.c0 = (b % tiles) * kColWidth;
+    b /= tiles;
+    cb.sl = b % slices;
+    cb.o = b / slices;
+    cb.d0 = cb.sl * dslice;
+    cb.d1 = cb.d0 + dslice < D ? cb.d0 + dslice : D;
+    return cb;
+}
+
+// (m, s) <- (m, s) merged with (m2, s2), each s a sum of exp(v - m).
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    if (mn == -INFINITY) return;
+    s = (m == -INFINITY ? 0.0f : s * exp_fast(m - mn)) + (m2 == -INFINITY ? 0.0f : s2 * exp_fast(m2 - mn));
+    m = mn;
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(kColWaves * kWave) void softmax_cols_kernel(
+    const typename Elem<T>::storage* x, typename Elem<T>::storage* y, float* pm, float* ps, int64_t outer,
+    int64_t D, int64_t inner, int64_t tiles, int64_t slices, int64_t dslice, bool log) {
+    __shared__ float sm[kColWaves][kColWidth], ss[kColWaves][kColWidth];
+    const ColBlock cb = col_block(tiles, slices, D, dslice);
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    const int64_t c = cb.c0 + lane;
+    const bool live = c < inner;
+    const int64_t base = cb.o * D * inner + (live ? c : inner - 1);
+    const typename Elem<T>::storage* col = x + base;
+    float m = -INFINITY, s = 0.0f;
+    if constexpr (MODE != kColWrite) {
+        for (int64_t d = cb.d0 + w; d < cb.d1; d += kColWaves * kColBatch) {
+            float v[kColBatch];
+#pragma unroll
+            for (int j = 0; j < kColBatch; ++j) {
+                const int64_t dj = d + j * kColWaves;
+                v[j] = Elem<T>::load(col[(dj < cb.d1 ? dj : cb.d1 - 1) * inner]);
             }
+            float bm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kColBatch; ++j) {
+                if (d + j * kColWaves >= cb.d1) v[j] = -INFINITY;
+                bm = fmaxf(bm, v[j]);
+            }
+            if (bm == -INFINITY) continue;
+            float bs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kColBatch; ++j) bs += exp_fast(v[j] - bm);
+            lse_merge(m, s, bm, bs);
         }
-        const float shift = m == -INFINITY ? 0.0f : m;
-        const float lse = logf(s);
-        const float inv = 1.0f / s;
-        for (int64_t d = 0; d < D; ++d) {
-            const float v = Elem<T>::load(x[base + d * inner]) - shift;
-            y[base + d * inner] = Elem<T>::store(log ? v - lse : exp_fast(v) * inv);
+        sm[w][lane] = m;
+        ss[w][lane] = s;
+        __syncthreads();
+        m = sm[0][lane];
+        s = ss[0][lane];
+#pragma unroll
+        for (int k = 1; k < kColWaves; ++k) lse_merge(m, s, sm[k][lane], ss[k][lane]);
+        if constexpr (MODE == kColStats) {
+            if (w == 0 && live) {
+                const int64_t at = (cb.sl * outer + cb.o) * inner + c;
+                pm[at] = m;
+                ps[at] = s;
+            }
+            return;
+        }
+    } else {
+        const int64_t cc = live ? c : inner - 1;
+        for (int64_t k = 0; k < slices; ++k) {
+            const int64_t at = (k * outer + cb.o) * inner + cc;
+            lse_merge(m, s, pm[at], ps[at]);
+        }
+    }
+    // A column of -inf (or an empty one) would give inf - inf; exp(-inf - 0)
+    // keeps it at 0 instead.
+    const float shift = m == -INFINITY ? 0.0f : m;
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
+    typename Elem<T>::storage* out = y + base;
+    for (int64_t d = cb.d0 + w; d < cb.d1; d += kColWaves * kColBatch) {
+        float v[kColBatch];
+#pragma unroll
+        for (int j = 0; j < kColBatch; ++j) {
+            const int64_t dj = d + j * kColWaves;
+            v[j] = Elem<T>::load(col[(dj < cb.d1 ? dj : cb.d1 - 1) * inner]) - shift;
+        }
+#pragma unroll
+        for (int j = 0; j < kColBatch; ++j) {
+            const int64_t dj = d + j * kColWaves;
+            if (live && dj < cb.d1) out[dj * inner] = Elem<T>::store(log ? v[j] - lse : exp_fast(v[j]) * inv);
         }
     }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void softmax_backward_strided_kernel(
-    const typename Elem<T>::storage* y, const typename Elem<T>::storage* dy,
-    typename Elem<T>::storage* dx, int64_t outer, int64_t D, int64_t inner, bool log) {
-    const int64_t total = outer * inner;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; t < total;
-         t += stride) {
-        const int64_t o = t / inner, i = t - o * inner;
-        const int64_t base = o * D * inner + i;
-        float s = 0.0f;
-        for (int64_t d = 0; d < D; ++d) {
-            const float g = Elem<T>::load(dy[base + d * inner]);
-            s += log ? g : g * Elem<T>::load(y[base + d * inner]);
+// The backward: per column s = sum over D of dy (log) or dy * y, then
+// dx = dy - exp(y) s (log) or y (dy - s).
+template <typename T, int MODE>
+__global__ __launch_bounds__(kColWaves * kWave) void softmax_backward_cols_kernel(
+    const typename Elem<T>::storage* y, const typename Elem<T>::storage* dy, typename Elem<T>::storage* dx,
+    float* ps, int64_t outer, int64_t D, int64_t inner, int64_t tiles, int64_t slices, int64_t dslice, bool log) {
+    __shared__ float ss[kColWaves][kColWidth];
+    const ColBlock cb = col_block(tiles, slices, D, dslice);
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    const int64_t c = cb.c0 + lane;
+    const bool live = c < inner;
+    const int64_t base = cb.o * D * inner + (live ? c : inner - 1);
+    const typename Elem<T>::storage* ycol = y + base;
+    const typename Elem<T>::storage* gcol = dy + base;
+    float s = 0.0f;
+    if constexpr (MODE != kColWrite) {
+        for (int64_t d = cb.d0 + w; d < cb.d1; d += kColWaves * kColBatch) {
+            float a[kColBatch], g[kColBatch];
+#pragma unroll
+            for (int j = 0; j < kColBatch; ++j) {
+                const int64_t dj = d + j * kColWaves;
+                const int64_t at = (dj < cb.d1 ? dj : cb.d1 - 1) * inner;
+                a[j] = Elem<T>::load(ycol[at]);
+                g[j] = Elem<T>::load(gcol[at]);
+            }
+#pragma unroll
+            for (int j = 0; j < kColBatch; ++j) {
+                if (d + j * kColWaves < cb.d1) s += log ? g[j] : g[j] * a[j];
+            }
         }
-        for (int64_t d = 0; d < D; ++d) {
-            const float a = Elem<T>::load(y[base + d * inner]);
-            const float g = Elem<T>::load(dy[base + d * inner]);
-            dx[base + d * inner] = Elem<T>::store(log ? g - exp_fast(a) * s : a * (g - s));
+        ss[w][lane] = s;
+        __syncthreads();
+        s = ss[0][lane];
+#pragma unroll
+        for (int k = 1; k < kColWaves; ++k) s += ss[k][lane];
+        if constexpr (MODE == kColStats) {
+            if (w == 0 && live) ps[(cb.sl * outer + cb.o) * inner + c] = s;
+            return;
+        }
+    } else {
+        const int64_t cc = live ? c : inner - 1;
+        for (int64_t k = 0; k < slices; ++k) s += ps[(k * outer + cb.o) * inner + cc];
+    }
+    typename Elem<T>::storage* out = dx + base;
+    for (int64_t d = cb.d0 + w; d < cb.d1; d += kColWaves * kColBatch) {
+        float a[kColBatch], g[kColBatch];
+#pragma unroll
+        for (int j = 0; j < kColBatch; ++j) {
+            const int64_t dj = d + j * kColWaves;
+            const int64_t at = (dj < cb.d1 ? dj : cb.d1 - 1) * inner;
+            a[j] = Elem<T>::load(ycol[at]);
+            g[j] = Elem<T>::load(gcol[at]);
+        }
+#pragma unroll
+        for (int j = 0; j < kColBatch; ++j) {
+            const int64_t dj = d + j * kColWaves;
+            if (live && dj < cb.d1) {
+                out[dj * inner] = Elem<T>::store(log ? g[j] - exp_fast(a[j]) * s : a[j] * (g[j] - s));
+            }
         }
     }
+}
+
+// Tiles, slices and rows a slice for the column kernels: enough blocks for
+// two a CU, slices of at least 64 rows.
+struct ColPlan {
+    int64_t tiles, slices, dslice, blocks;
+};
+
+ColPlan col_plan(int64_t outer, int64_t D, int64_t inner, int device) {
+    ColPlan p;
+    p.tiles = (inner + kColWidth - 1) / kColWidth;
+    const int64_t base = outer * p.tiles;
+    const int64_t want = 2 * static_cast<int64_t>(cu_count(device));
+    int64_t slices = (want + base - 1) / base;
+    const int64_t most = (D + 63) / 64;
+    if (slices > most) slices = most;
+    if (slices < 1) slices = 1;
+    p.dslice = (D + slices - 1) / slices;
+    p.slices = (D + p.dslice - 1) / p.dslice;
+    p.blocks = base * p.slices;
+    return p;
 }
 
 // ---- configuration choice ---------------------------------------------------
@@ -691,12 +841,6 @@ RowConfig choose_config(int64_t D) {
     return RowConfig{0, 0};
 }
 
-int64_t strided_grid(int64_t total, int device) {
-    const int64_t want = (total + kBlock - 1) / kBlock;
-    const int64_t cap = static_cast<int64_t>(cu_count(device)) * 32;
-    return want < cap ? (want > 0 ? want : 1) : cap;
-}
-
 template <typename T>
 void softmax_typed(int device, bool log, int64_t outer, int64_t D, int64_t inner, const void* x,
                    void* y) {
@@ -730,8 +874,24 @@ void softmax_typed(int device, bool log, int64_t outer, int64_t D, int64_t inner
                 static_cast<const S*>(x), static_cast<S*>(y), D, log);
         }
     } else {
-        softmax_strided_kernel<T><<<strided_grid(outer * inner, device), kBlock, 0, st>>>(
-            static_cast<const S*>(x), static_cast<S*>(y), outer, D, inner, log);
+        const ColPlan cp = col_plan(outer, D, inner, device);
+        TP_AMD_CHECK(cp.blocks < (int64_t{1} << 31), "softmax: ", cp.blocks, " blocks exceed the grid");
+        const unsigned blocks = static_cast<unsigned>(cp.blocks);
+        if (cp.slices == 1) {
+            softmax_cols_kernel<T, kColFused><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(x), static_cast<S*>(y), nullptr, nullptr, outer, D, inner, cp.tiles, 1, cp.dslice,
+                log);
+        } else {
+            const size_t parts = static_cast<size_t>(cp.slices * outer * inner);
+            Workspace ws(2 * parts * sizeof(float), device);
+            float* pm = static_cast<float*>(ws.get());
+            float* ps = pm + parts;
+            softmax_cols_kernel<T, kColStats><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(x), nullptr, pm, ps, outer, D, inner, cp.tiles, cp.slices, cp.dslice, log);
+            softmax_cols_kernel<T, kColWrite><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(x), static_cast<S*>(y), pm, ps, outer, D, inner, cp.tiles, cp.slices, cp.dslice,
+                log);
+        }
     }
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
@@ -765,9 +925,23 @@ void softmax_backward_typed(int device, bool log, int64_t outer, int64_t D, int6
                 static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), D, log);
         }
     } else {
-        softmax_backward_strided_kernel<T><<<strided_grid(outer * inner, device), kBlock, 0, st>>>(
-            static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), outer, D,
-            inner, log);
+        const ColPlan cp = col_plan(outer, D, inner, device);
+        TP_AMD_CHECK(cp.blocks < (int64_t{1} << 31), "softmax backward: ", cp.blocks, " blocks exceed the grid");
+        const unsigned blocks = static_cast<unsigned>(cp.blocks);
+        if (cp.slices == 1) {
+            softmax_backward_cols_kernel<T, kColFused><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), nullptr, outer, D, inner,
+                cp.tiles, 1, cp.dslice, log);
+        } else {
+            Workspace ws(static_cast<size_t>(cp.slices * outer * inner) * sizeof(float), device);
+            float* ps = static_cast<float*>(ws.get());
+            softmax_backward_cols_kernel<T, kColStats><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(y), static_cast<const S*>(dy), nullptr, ps, outer, D, inner, cp.tiles,
+                cp.slices, cp.dslice, log);
+            softmax_backward_cols_kernel<T, kColWrite><<<blocks, kColWaves * kWave, 0, st>>>(
+                static_cast<const S*>(y), static_cast<const S*>(dy), static_cast<S*>(dx), ps, outer, D, inner,
+                cp.tiles, cp.slices, cp.dslice, log);
+        }
     }
     TP_AMD_HIP_CHECK(hipGetLastError());
 }

@@ -6,7 +6,7 @@ reference's norm-wise rule (tests/_check.py)."""
 import numpy as np
 import pytest
 
-from _check import BF16, F16, F32, assert_bitexact, assert_normwise, assert_sum
+from _check import BF16, F16, F32, as_float, assert_bitexact, assert_normwise, assert_sum
 
 pytestmark = pytest.mark.gpu
 
@@ -202,17 +202,34 @@ def test_amax_amin_nan_and_signed_zero_vectorised(dev, ops, orc, dtype, dim):
         assert_bitexact(got[ok], want[ok], f"op {op} dim {dim}")
 
 
+# Shapes for softmax over dim 0 / 1 (inner > 1): one column tile of one
+# slice; several tiles; few tiles over a long D, split into slices whose
+# partials a second launch folds; an odd inner size; enough tiles for one
+# fused launch.
+SOFTMAX_SHAPES = [(5, 6, 7), (3, 90, 130), (300, 2, 130), (700, 3, 37), (64, 1000, 64)]
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("dim", [0, 1, -1])
-def test_softmax_and_log_softmax(dev, ops, orc, dtype, dim):
-    a = sample(orc, (5, 6, 7), dtype)
+@pytest.mark.parametrize("shape", SOFTMAX_SHAPES, ids=["5x6x7", "3x90x130", "300x2x130", "700x3x37",
+                                                       "64x1000x64"])
+def test_softmax_and_log_softmax(dev, ops, orc, dtype, dim, shape):
+    a = sample(orc, shape, dtype)
+    if shape == (300, 2, 130):
+        # -inf over half a column: over dim 0, whole slices of it hold only -inf
+        a[:150, 1, 5] = orc.from_float(np.full(150, -np.inf, np.float32), dtype)
     d = dev.from_numpy(a, dtype=dtype)
     k = dim % 3
     outer, size, inner = int(np.prod(a.shape[:k])), a.shape[k], int(np.prod(a.shape[k + 1:]))
     for log, fn in ((False, ops.softmax), (True, ops.log_softmax)):
         y = fn(d, dim)
         want = orc.softmax(log, dtype, a, outer, size, inner)
-        assert_normwise(y.numpy(), want, dtype, 1, f"softmax log={log}")
+        # log_softmax of -inf is -inf: infinities must match in place and
+        # sign, the finite entries norm-wise
+        got_f, want_f = as_float(y.numpy(), dtype), as_float(want, dtype)
+        inf = np.isinf(want_f)
+        assert np.array_equal(np.isinf(got_f), inf) and np.array_equal(got_f[inf], want_f[inf]), "infinities"
+        assert_normwise(y.numpy()[~inf], want[~inf], dtype, 1, f"softmax log={log}")
         g = sample(orc, a.shape, dtype, 9)
         back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
         got = back(dev.from_numpy(g, dtype=dtype), y, dim, dtype).numpy()
