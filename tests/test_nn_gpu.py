@@ -44,8 +44,9 @@ LN_CASES = [
     ((9, 1001), (1001,)),        # width not a whole number of packets
     ((37, 12288), (12288,)),     # sixteen waves a row, the widest register layouts
     ((2, 40000), (40000,)),      # a row longer than the register-resident kernel holds
+    ((300, 9000), (9000,)),      # the backward's generic dW/dB pass over four row slices
 ]
-LN_IDS = ["4x16", "3x5x24", "300x1024", "64x4096", "9x1001", "37x12288", "2x40000"]
+LN_IDS = ["4x16", "3x5x24", "300x1024", "64x4096", "9x1001", "37x12288", "2x40000", "300x9000"]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
