@@ -24,12 +24,82 @@ void reduce_run(const TensorRef& x, const Sizes& shape, int first, int last, int
     TP_AMD_CHECK(st == TP_AMD_OK, last_error());
 }
 
+// When ``t`` is a permutation of a dense tensor (its strides, largest
+// first, are the row-major strides of its sizes in that order), the dims in
+// memory order, outermost first; otherwise empty.
+std::vector<int> dense_order(const TensorRef& t) {
+    const int nd = t.ndim;
+    std::vector<int> order(nd);
+    for (int i = 0; i < nd; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+        // size-1 dims last, they hold no layout
+        if ((t.sizes[a] == 1) != (t.sizes[b] == 1)) return t.sizes[b] == 1;
+        return t.strides[a] > t.strides[b];
+    });
+    int64_t expected = 1;
+    for (int i = nd - 1; i >= 0; --i) {
+        const int d = order[i];
+        if (t.sizes[d] == 1) continue;
+        if (t.strides[d] != expected) return {};
+        expected *= t.sizes[d];
+    }
+    return order;
+}
+
+Owned reduce_dense(const TensorRef& x, Sizes dims, bool keepdim, int op, int out_dtype, int device);
+
 // Reduce ``self`` over ``dims`` (all when empty) into a keepdim-shaped
 // tensor, then view it without the reduced dimensions unless keepdim
 // (reduce(), :47-84).  The input is converted to the result dtype first.
 // Reduced dims that are not adjacent take one pass per run of adjacent
-// reduced dims, innermost run first, with float32 intermediates.
+// reduced dims, innermost run first, with float32 intermediates.  A
+// non-contiguous input that is a permutation of a dense tensor (a
+// transpose) is reduced where it lies, its dims taken in memory order, and
+// only the (smaller) result is reordered if its kept dims come out of
+// order; other strided inputs are copied dense first.
 Owned reduce(const TensorRef& self, Sizes dims, bool keepdim, int op, int out_dtype) {
+    const int nd = self.ndim;
+    if (nd > 1 && self.dtype == out_dtype && !is_contiguous(self) && numel(self) > 0) {
+        const std::vector<int> order = dense_order(self);
+        if (!order.empty()) {
+            std::vector<bool> reduced(nd, dims.empty());
+            for (int64_t d : dims) {
+                const int64_t k = d < 0 ? d + nd : d;
+                TP_AMD_CHECK(k >= 0 && k < nd, "dimension ", d, " out of range for a ", nd, "-d tensor");
+                reduced[k] = true;
+            }
+            // The same bytes viewed in memory order, and the dims to reduce there.
+            Sizes psizes(nd), pstrides(nd), pdims;
+            for (int i = 0; i < nd; ++i) {
+                psizes[i] = self.sizes[order[i]];
+                pstrides[i] = self.strides[order[i]];
+                if (reduced[order[i]]) pdims.push_back(i);
+            }
+            TensorRef dense = make_view(self, psizes, pstrides);
+            dense.ctx = self.ctx;
+            Owned pout = reduce_dense(dense, pdims, true, op, out_dtype, self.device);
+            // pout: keepdim result in memory order; view it in logical order.
+            Sizes keep(nd), kstrides(nd);
+            for (int i = 0; i < nd; ++i) keep[i] = reduced[i] ? 1 : self.sizes[i];
+            const Sizes pstr = contiguous_strides(sizes_of(pout.ref()));
+            for (int i = 0; i < nd; ++i) kstrides[order[i]] = pstr[i];
+            TensorRef logical = make_view(pout.ref(), keep, kstrides);
+            Owned out = empty_on(keep, out_dtype, self.device);
+            strided_copy(out.ref(), logical);  // one memcpy when the order already matches
+            if (keepdim) return out;
+            Sizes final_shape;
+            for (int i = 0; i < nd; ++i)
+                if (!reduced[i]) final_shape.push_back(self.sizes[i]);
+            TensorRef view = make_view(out.ref(), final_shape, contiguous_strides(final_shape));
+            view.ctx = out.ref().ctx;
+            out.release();
+            return Owned(view);
+        }
+    }
+    return reduce_dense(self, std::move(dims), keepdim, op, out_dtype, self.device);
+}
+
+Owned reduce_dense(const TensorRef& self, Sizes dims, bool keepdim, int op, int out_dtype, int) {
     const int nd = self.ndim;
     MaybeOwned converted = to_dtype(self, out_dtype);
     MaybeOwned x = contiguous_on_device(converted.ref);

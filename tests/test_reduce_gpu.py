@@ -202,6 +202,30 @@ def test_amax_amin_nan_and_signed_zero_vectorised(dev, ops, orc, dtype, dim):
         assert_bitexact(got[ok], want[ok], f"op {op} dim {dim}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reductions_of_permuted_views(dev, ops, orc, dtype):
+    """A transposed or permuted view of a dense tensor is reduced where it
+    lies, its dims in memory order; the result comes back in logical order
+    (reordered when its kept dims lie out of order).  Sums at the sum
+    tolerance, amax / amin bit-exact."""
+    a = sample(orc, (64, 96), dtype, 11)
+    d = dev.from_numpy(a, dtype=dtype)
+    at = np.ascontiguousarray(a.T)
+    for dims in ([0], [1], None):
+        assert_sum(ops.sum_dim(d.t(), dims or []).numpy() if dims else ops.sum(d.t()).numpy(),
+                   oracle_reduce(orc, SUM, dtype, at, dims), dtype, f"sum of .t() over {dims}")
+    assert_bitexact(ops.amax(d.t(), [0]).numpy(), oracle_reduce(orc, AMAX, dtype, at, [0]), "amax of .t()")
+    b = sample(orc, (6, 40, 24), dtype, 12)
+    db = dev.from_numpy(b, dtype=dtype)
+    perm = db._view([24, 6, 40], [1, 960, 24])      # b.transpose(2, 0, 1), no copy
+    bp = np.ascontiguousarray(np.transpose(b, (2, 0, 1)))
+    assert_sum(ops.sum_dim(perm, [1]).numpy(), oracle_reduce(orc, SUM, dtype, bp, [1]), dtype,
+               "sum over dim 1 of a permutation (kept dims reordered)")
+    got = ops.sum_dim(perm, [0, 2], keepdim=True).numpy()
+    assert_sum(got, oracle_reduce(orc, SUM, dtype, bp, [0, 2], True), dtype, "sum (0, 2) of a permutation")
+    assert_bitexact(ops.amin(perm, [2]).numpy(), oracle_reduce(orc, AMIN, dtype, bp, [2]), "amin of a permutation")
+
+
 # Shapes for softmax over dim 0 / 1 (inner > 1): one column tile of one
 # slice; several tiles; few tiles over a long D, split into slices whose
 # partials a second launch folds; an odd inner size; enough tiles for one
