@@ -165,11 +165,12 @@ private:
         for (int id = 1; id < parts_; ++id) std::thread([this, id] { work(id); }).detach();
     }
 
-    // Part `id` of the current copy, in 64-byte multiples.  dst_, src_ and
-    // n_ were written under m_ before the generation moved on, and a worker
-    // reads them after seeing the new generation under m_.
+    // Part `id` of the current copy, in 64-byte multiples; the parts cover
+    // all n_ bytes (per >= ceil(n_ / parts_)).  dst_, src_ and n_ were
+    // written under m_ before the generation moved on, and a worker reads
+    // them after seeing the new generation under m_.
     void copy_part(int id) const {
-        const size_t per = (n_ / parts_ + 63) & ~size_t{63};
+        const size_t per = ((n_ + parts_ - 1) / parts_ + 63) & ~size_t{63};
         const size_t lo = std::min(n_, per * id), hi = std::min(n_, lo + per);
         if (hi > lo) std::memcpy(dst_ + lo, src_ + lo, hi - lo);
     }

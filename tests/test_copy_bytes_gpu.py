@@ -5,7 +5,9 @@ bit-exact on random bytes; odd sizes and unaligned offsets on both sides;
 64 MiB, the size of the reference README's h2d / d2h rows; sizes either side
 of 8 MiB, from which host copies go through four pinned 4 MiB chunks, and
 one of 18 chunks (each chunk buffer reused four or five times in each
-direction); a zero-byte copy is a no-op."""
+direction); two sizes whose last chunk (262,148 and 4,177,924 bytes) does
+not split into eight equal 64-byte multiples over the host copy threads; a
+zero-byte copy is a no-op."""
 
 import ctypes as C
 
@@ -23,8 +25,9 @@ def _host_ptr(buf: np.ndarray, offset: int = 0) -> C.c_void_p:
 
 
 @pytest.mark.parametrize("nbytes", [1, 3, 4097, (1 << 20) + 7, (8 << 20) - 1, 8 << 20, (8 << 20) + 1,
-                                    64 << 20, (68 << 20) + 5],
-                         ids=["1B", "3B", "4097B", "1MiB+7", "8MiB-1", "8MiB", "8MiB+1", "64MiB", "68MiB+5"])
+                                    64 << 20, (68 << 20) + 5, (8 << 20) + 262148, 2047 * 2047 * 4],
+                         ids=["1B", "3B", "4097B", "1MiB+7", "8MiB-1", "8MiB", "8MiB+1", "64MiB", "68MiB+5",
+                              "8MiB+256KiB+4", "2047^2-fp32"])
 @pytest.mark.parametrize("offset", [0, 3], ids=["aligned", "offset3"])
 def test_round_trip_is_bit_exact(amd, dev, ops, nbytes, offset):
     lib = amd.load()
