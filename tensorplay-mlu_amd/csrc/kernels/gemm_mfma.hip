@@ -50,6 +50,7 @@
 #include "../allocator.h"
 #include "../common.h"
 #include "../runtime.h"
+#include "tp_amd_kernels.h"
 
 namespace tp_amd {
 
@@ -898,16 +899,23 @@ void launch(const GemmArgs& p, hipStream_t stream) {
 
 }  // namespace smallk
 
+// An operand the matrix-core kernels read in place: 16-byte aligned, and its
+// leading dimension, batch stride and contiguous extent (K when K-major, M or
+// N otherwise) whole numbers of V-element packets.
+template <typename T>
+bool operand_ok(const void* ptr, int64_t ld, int64_t stride, bool kmajor, int64_t mn, int64_t k) {
+    constexpr int V = Mfma<T>::V;
+    return aligned16(ptr) && ld % V == 0 && stride % V == 0 && (kmajor ? k : mn) % V == 0;
+}
+
+bool tiles_fit(const GemmArgs& p) {
+    return (p.m + 127) / 128 * ((p.n + 127) / 128) < (int64_t(1) << 31);
+}
+
 template <typename T>
 bool mfma_eligible(const GemmArgs& p) {
-    constexpr int V = Mfma<T>::V;
-    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
-    auto ok = [&](const void* ptr, int64_t ld, int64_t stride, bool kmajor, int64_t mn) {
-        return aligned16(ptr) && ld % V == 0 && stride % V == 0 && (kmajor ? p.k % V == 0 : mn % V == 0);
-    };
-    return p.k > 0 && ok(p.a, p.lda, p.stride_a, a_kmajor, p.m) &&
-           ok(p.b, p.ldb, p.stride_b, b_kmajor, p.n) &&
-           (p.m + 127) / 128 * ((p.n + 127) / 128) < (int64_t(1) << 31);
+    return p.k > 0 && operand_ok<T>(p.a, p.lda, p.stride_a, !p.trans_a, p.m, p.k) &&
+           operand_ok<T>(p.b, p.ldb, p.stride_b, p.trans_b, p.n, p.k) && tiles_fit(p);
 }
 
 template <typename T, int BM, int BN, int WM, int WN>
@@ -1062,10 +1070,78 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     launch_config<T, 128, 128, 2, 2>(p, stream);
 }
 
+// Products with an operand the matrix-core kernels cannot read in place (an
+// odd K or leading dimension: a vocabulary of 50257, a Linear(1023, ...), a
+// column slice at an odd offset) copy that operand into a dense K-major
+// workspace [batch][M or N][K'], K' = K rounded up to the packet, with the
+// columns K..K' zeroed; an odd K repacks both operands, so the padded terms
+// are 0 x 0.  The copies cost a pass over the operands; the general kernel
+// they replace runs ~16x slower than the matrix cores (2047^3 in bfloat16:
+// 692 us there, 63 us repacked).  Products under kRepackMinMacs
+// multiply-adds (about 160^3) keep the general kernel, which needs no
+// workspace and no extra launches: measured, 130^3 is 2 us faster there and
+// 200^3 7 us faster repacked.
+constexpr double kRepackMinMacs = double(int64_t(1) << 22);
+
+void check_status(int status) { TP_AMD_CHECK(status == 0, last_error()); }
+
+// x logical [bs][rows][k] (element (b, r, j) at x + b stride + r ld + j when
+// K-major, + j ld + r otherwise) -> ws [bs][rows][kp], columns k..kp zero.
+void repack_kmajor(int device, int esize, const void* x, int64_t ld, int64_t stride, bool kmajor,
+                   int64_t bs, int64_t rows, int64_t k, int64_t kp, void* ws) {
+    const int64_t sizes[3] = {bs, rows, k};
+    const int64_t dst[3] = {rows * kp, kp, 1};
+    const int64_t src[3] = {stride, kmajor ? ld : 1, kmajor ? 1 : ld};
+    check_status(tp_amd_launch_strided_copy(device, esize, 3, sizes, ws, dst, x, src));
+    if (kp > k) {
+        const uint64_t zero = 0;
+        const int64_t pad[3] = {bs, rows, kp - k};
+        check_status(tp_amd_launch_fill(device, esize, &zero, 3, pad, static_cast<char*>(ws) + k * esize, dst));
+    }
+}
+
+template <typename T>
+void launch_repacked(const GemmArgs& p, hipStream_t stream) {
+    constexpr int V = Mfma<T>::V;
+    constexpr int E = sizeof(typename Elem<T>::storage);
+    int device = 0;
+    TP_AMD_HIP_CHECK(hipGetDevice(&device));
+    const int64_t kp = (p.k + V - 1) / V * V;
+    const bool fix_a = kp != p.k || !operand_ok<T>(p.a, p.lda, p.stride_a, !p.trans_a, p.m, p.k);
+    const bool fix_b = kp != p.k || !operand_ok<T>(p.b, p.ldb, p.stride_b, p.trans_b, p.n, p.k);
+    // A batch-broadcast operand (stride 0) is copied once and stays broadcast.
+    const int64_t bs_a = p.stride_a == 0 ? 1 : p.batch, bs_b = p.stride_b == 0 ? 1 : p.batch;
+    const size_t bytes_a = fix_a ? static_cast<size_t>(bs_a * p.m * kp) * E : 0;
+    const size_t off_b = (bytes_a + 255) / 256 * 256;
+    const size_t bytes_b = fix_b ? static_cast<size_t>(bs_b * p.n * kp) * E : 0;
+    Workspace ws(off_b + bytes_b, device);
+    GemmArgs q = p;
+    q.k = kp;
+    if (fix_a) {
+        repack_kmajor(device, E, p.a, p.lda, p.stride_a, !p.trans_a, bs_a, p.m, p.k, kp, ws.get());
+        q.a = ws.get();
+        q.lda = kp;
+        q.stride_a = p.stride_a == 0 ? 0 : p.m * kp;
+        q.trans_a = false;
+    }
+    if (fix_b) {
+        void* wb = static_cast<char*>(ws.get()) + off_b;
+        repack_kmajor(device, E, p.b, p.ldb, p.stride_b, p.trans_b, bs_b, p.n, p.k, kp, wb);
+        q.b = wb;
+        q.ldb = kp;
+        q.stride_b = p.stride_b == 0 ? 0 : p.n * kp;
+        q.trans_b = true;
+    }
+    launch_mfma<T>(q, stream);
+}
+
 template <typename T>
 void launch_typed(const GemmArgs& p, hipStream_t stream) {
     if (mfma_eligible<T>(p)) {
         launch_mfma<T>(p, stream);
+    } else if (p.k > 0 && tiles_fit(p) &&
+               double(p.batch) * double(p.m) * double(p.n) * double(p.k) >= kRepackMinMacs) {
+        launch_repacked<T>(p, stream);
     } else {
         launch_gemm_general<T>(p, stream);
     }

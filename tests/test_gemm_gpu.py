@@ -244,6 +244,51 @@ def test_gemm_abi_padded_batched(amd, dev, orc, dtype, ta, tb, bt, m, n, k):
     check(orc, got, want, dtype, f"gemm abi {bt}x{m}x{n}x{k} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("bt,m,n,k,pad,bcast", [(1, 515, 517, 509, 3, False), (1, 520, 512, 512, 3, False),
+                                                (4, 300, 270, 255, 5, True)],
+                         ids=["odd-K", "odd-ld", "odd-K-batch-broadcast"])
+def test_gemm_abi_repacked_operands(amd, dev, orc, dtype, ta, tb, bt, m, n, k, pad, bcast):
+    """Products whose operands the matrix-core kernels cannot read in place
+    (odd K, odd leading dimensions, NaN in the padding) are repacked into
+    aligned K-major copies, K padded with zeros: alpha = 0.5, beta = 2 with
+    a full Cin, and in the batched case a B broadcast over the batch
+    (stride 0)."""
+    lib = amd.load()
+    alpha, beta = 0.5, 2.0
+    a = _padded(orc, (bt, k, m) if ta else (bt, m, k), pad, dtype, 1)
+    b = _padded(orc, (1 if bcast else bt, n, k) if tb else (1 if bcast else bt, k, n), pad, dtype, 2)
+    cin = sample(orc, (bt, m, n), dtype, 3)
+    lda, ldb = a.shape[-1], b.shape[-1]
+    da, db, dc = (dev.from_numpy(x, dtype=dtype) for x in (a, b, cin))
+    out = dev.empty((bt, m, n), dtype=dtype)
+    st = lib.tp_amd_launch_gemm(0, dtype, bt, m, n, k, alpha, da.data_ptr, lda, a.shape[-2] * lda,
+                                int(ta), db.data_ptr, ldb, 0 if bcast else b.shape[-2] * ldb, int(tb),
+                                beta, dc.data_ptr, n, 1, m * n, out.data_ptr, n, m * n)
+    assert st == 0, lib.tp_mlu_last_error()
+    A = orc.to_float(a, dtype)[..., :(m if ta else k)]
+    B = orc.to_float(b, dtype)[..., :(k if tb else n)]
+    A = np.swapaxes(A, -1, -2) if ta else A
+    B = np.swapaxes(B, -1, -2) if tb else B
+    want = alpha * np.matmul(A, B) + beta * orc.to_float(cin, dtype)
+    got = out.numpy()
+    assert not np.isnan(orc.to_float(got, dtype)).any(), "padding leaked into the product"
+    check(orc, got, want, dtype, f"gemm abi {bt}x{m}x{n}x{k} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_mm_2047_cube(dev, ops, orc, dtype):
+    """mm 2047^3 (odd everything) through ops.mm, checked on sampled
+    entries and with Freivalds' test."""
+    a = sample(orc, (2047, 2047), dtype, 11, 0.05)
+    b = sample(orc, (2047, 2047), dtype, 12, 0.05)
+    got = ops.mm(dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)).numpy()
+    assert sampled_entries(orc, got, a, b, dtype) <= BAR[dtype]
+    assert freivalds(orc, got, a, b, dtype) <= BAR[dtype]
+
+
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["NN", "TN", "NT", "TT"])
 @pytest.mark.parametrize("cin_kind", ["full", "bias-row"])
