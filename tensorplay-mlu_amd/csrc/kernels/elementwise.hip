@@ -367,6 +367,110 @@ bool try_binary2d(int device, int ma, int mb, const void* a, const void* b, void
     return false;
 }
 
+// out [rows][cols] (row stride ldo) = f(a, b), where an input is read
+// row-major (element (r, c) at x[r ld + c]; ld may be 0, a row broadcast) or
+// column-major (at x[c ld + r]: a transposed view such as x.t() + y).  One
+// 64 x 64 tile a block: the column-major inputs are read along r, their
+// unit-stride axis, into LDS as floats; then consecutive threads walk c for
+// the row-major inputs and the output, so every HBM access is coalesced.
+// The tile rows are 65 floats apart, so the transposed LDS reads of a wave
+// fall in 64 different banks.  Tiles run in diagonal order (block b takes
+// tile row b % gy, tile column (b / gy + b % gy) % gx) so that blocks that
+// run together read the column-major inputs at different offsets.
+constexpr int kTTile = 64;
+
+template <typename T, bool ACOL, bool BCOL, typename F>
+__global__ __launch_bounds__(kBlock) void binary_transposed_kernel(
+    const typename Elem<T>::storage* __restrict__ a, int64_t lda,
+    const typename Elem<T>::storage* __restrict__ b, int64_t ldb,
+    typename Elem<T>::storage* __restrict__ out, int64_t ldo, int64_t rows, int64_t cols, F f) {
+    using S = typename Elem<T>::storage;
+    constexpr int kStep = kBlock / kTTile;  // 4 rows of the tile at a time
+    constexpr int kPer = kTTile / kStep;    // 16 elements a thread
+    __shared__ float ta[ACOL ? kTTile : 1][kTTile + 1];
+    __shared__ float tb[BCOL ? kTTile : 1][kTTile + 1];
+    const int64_t bid = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t ty_tile = bid % gridDim.y, tx_tile = (bid / gridDim.y + ty_tile) % gridDim.x;
+    const int64_t r0 = ty_tile * kTTile, c0 = tx_tile * kTTile;
+    const int tx = threadIdx.x % kTTile, ty = threadIdx.x / kTTile;
+    const bool full = r0 + kTTile <= rows && c0 + kTTile <= cols;
+    auto stage = [&](const S* x, int64_t ld, float (*tile)[kTTile + 1]) {
+        S v[kPer];
+        if (full) {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) v[k] = x[(c0 + ty + k * kStep) * ld + r0 + tx];
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int64_t r = r0 + tx, c = c0 + ty + k * kStep;
+                v[k] = r < rows && c < cols ? x[c * ld + r] : S{};
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) tile[ty + k * kStep][tx] = Elem<T>::load(v[k]);
+    };
+    if constexpr (ACOL) stage(a, lda, ta);
+    if constexpr (BCOL) stage(b, ldb, tb);
+    __syncthreads();
+    const int64_t c = c0 + tx;
+    S ra[kPer], rb[kPer];
+    if constexpr (!ACOL || !BCOL) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int64_t r = r0 + ty + k * kStep;
+            const bool in = full || (r < rows && c < cols);
+            if constexpr (!ACOL) ra[k] = in ? a[r * lda + c] : S{};
+            if constexpr (!BCOL) rb[k] = in ? b[r * ldb + c] : S{};
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int64_t r = r0 + ty + k * kStep;
+        const float va = ACOL ? ta[tx][ty + k * kStep] : Elem<T>::load(ra[k]);
+        const float vb = BCOL ? tb[tx][ty + k * kStep] : Elem<T>::load(rb[k]);
+        if (full || (r < rows && c < cols)) out[r * ldo + c] = Elem<T>::store(f(va, vb));
+    }
+}
+
+// The two-dimensional case with a row-major output and at least one
+// column-major input; false when the layout is anything else.
+template <typename T, typename F>
+bool try_binary_transposed(int device, const Layout<3>& l, const void* a, const void* b, void* out,
+                           F f) {
+    using S = typename Elem<T>::storage;
+    if constexpr (sizeof(S) > 4) {
+        return false;
+    } else {
+        if (l.ndim != 2) return false;
+        const int64_t R = l.sizes[0], C = l.sizes[1];
+        const int64_t* so = l.strides[0];
+        const int64_t* sa = l.strides[1];
+        const int64_t* sb = l.strides[2];
+        if (so[1] != 1 || so[0] < C) return false;
+        auto col = [&](const int64_t* st) { return st[0] == 1 && st[1] >= R; };
+        auto row = [&](const int64_t* st) { return st[1] == 1 && st[0] >= 0; };
+        const bool acol = col(sa), bcol = col(sb);
+        if (!(acol || bcol) || !(acol || row(sa)) || !(bcol || row(sb))) return false;
+        const int64_t gx = (C + kTTile - 1) / kTTile, gy = (R + kTTile - 1) / kTTile;
+        if (gy > 65535 || gx * gy >= (int64_t(1) << 31)) return false;
+        const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+        const S* pa = static_cast<const S*>(a);
+        const S* pb = static_cast<const S*>(b);
+        S* po = static_cast<S*>(out);
+        const int64_t lda = acol ? sa[1] : sa[0], ldb = bcol ? sb[1] : sb[0];
+        hipStream_t st = stream(device);
+        if (acol && bcol) {
+            binary_transposed_kernel<T, true, true, F><<<grid, kBlock, 0, st>>>(pa, lda, pb, ldb, po, so[0], R, C, f);
+        } else if (acol) {
+            binary_transposed_kernel<T, true, false, F><<<grid, kBlock, 0, st>>>(pa, lda, pb, ldb, po, so[0], R, C, f);
+        } else {
+            binary_transposed_kernel<T, false, true, F><<<grid, kBlock, 0, st>>>(pa, lda, pb, ldb, po, so[0], R, C, f);
+        }
+        TP_AMD_HIP_CHECK(hipGetLastError());
+        return true;
+    }
+}
+
 template <typename T, typename F>
 void binary_typed(int device, int ndim, const int64_t* sizes, const void* a,
                   const int64_t* as, const void* b, const int64_t* bs, void* out,
@@ -394,6 +498,7 @@ void binary_typed(int device, int ndim, const int64_t* sizes, const void* a,
             return;
         }
     }
+    if (try_binary_transposed<T, F>(device, l, a, b, out, f)) return;
     if (!try_rows_nd<T, 2, F>(device, l, out, a, b, n, f)) launch_nd<T, 2, F>(device, l, out, a, b, n, f);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }

@@ -122,6 +122,32 @@ def test_row_padded_views_in_packets(dev, ops, orc, dtype):
     assert_bitexact(ops.relu(view).numpy(), orc.unary(8, dtype, a), "relu of a view")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(64, 64), (300, 200), (1000, 77), (5, 130)])
+def test_transposed_operands_in_tiles(dev, ops, orc, dtype, rows, cols):
+    """Binary ops with a transposed (column-major) operand into a row-major
+    output, which run through LDS tiles of 64 x 64: either side transposed,
+    both, a transposed operand with a broadcast row, a transposed slice of
+    a wider matrix, and an in-place update.  Bit-exact against the oracle."""
+    x = sample(orc, (cols, rows), dtype, 1)       # stored [cols][rows]; used as x.T
+    y = sample(orc, (rows, cols), dtype, 2)
+    z = sample(orc, (cols, rows), dtype, 3, 0.5, 2.0)
+    bias = sample(orc, (1, cols), dtype, 4)
+    dx, dy, dz = up(dev, x, dtype), up(dev, y, dtype), up(dev, z, dtype)
+    xt, zt = np.ascontiguousarray(x.T), np.ascontiguousarray(z.T)
+    assert_bitexact(ops.add(dx.t(), dy).numpy(), orc.binary(ADD, dtype, xt, y, 1.0), "x.t() + y")
+    assert_bitexact(ops.mul(dy, dx.t()).numpy(), orc.binary(MUL, dtype, y, xt), "y * x.t()")
+    assert_bitexact(ops.div(dx.t(), dz.t()).numpy(), orc.binary(DIV, dtype, xt, zt), "x.t() / z.t()")
+    assert_bitexact(ops.add(dx.t(), up(dev, bias, dtype)).numpy(), orc.binary(ADD, dtype, xt, bias, 1.0),
+                    "x.t() + row")
+    wide = sample(orc, (cols, rows + 9), dtype, 5)
+    wt = np.ascontiguousarray(wide[:, 3:3 + rows].T)
+    got = ops.add(up(dev, wide, dtype)[:, 3:3 + rows].t(), dy).numpy()
+    assert_bitexact(got, orc.binary(ADD, dtype, wt, y, 1.0), "slice.t() + y")
+    ops.add_(dy, dx.t())
+    assert_bitexact(dy.numpy(), orc.binary(ADD, dtype, y, xt, 1.0), "y.add_(x.t())")
+
+
 def test_strided_operands(dev, ops, orc):
     a = sample(orc, (5, 7), F32)
     d = up(dev, a, F32)
