@@ -128,7 +128,9 @@ def test_transposed_operands_in_tiles(dev, ops, orc, dtype, rows, cols):
     """Binary ops with a transposed (column-major) operand into a row-major
     output, which run through LDS tiles of 64 x 64: either side transposed,
     both, a transposed operand with a broadcast row, a transposed slice of
-    a wider matrix, and an in-place update.  Bit-exact against the oracle."""
+    a wider matrix (at odd and even offsets: 16-bit types with even sizes
+    and 4-byte aligned rows take 64 x 128 tiles of element pairs), and an
+    in-place update.  Bit-exact against the oracle."""
     x = sample(orc, (cols, rows), dtype, 1)       # stored [cols][rows]; used as x.T
     y = sample(orc, (rows, cols), dtype, 2)
     z = sample(orc, (cols, rows), dtype, 3, 0.5, 2.0)
@@ -144,6 +146,10 @@ def test_transposed_operands_in_tiles(dev, ops, orc, dtype, rows, cols):
     wt = np.ascontiguousarray(wide[:, 3:3 + rows].T)
     got = ops.add(up(dev, wide, dtype)[:, 3:3 + rows].t(), dy).numpy()
     assert_bitexact(got, orc.binary(ADD, dtype, wt, y, 1.0), "slice.t() + y")
+    wide2 = sample(orc, (cols, rows + 10), dtype, 6)
+    w2 = np.ascontiguousarray(wide2[:, 2:2 + rows].T)
+    got = ops.mul(dy, up(dev, wide2, dtype)[:, 2:2 + rows].t()).numpy()
+    assert_bitexact(got, orc.binary(MUL, dtype, y, w2), "y * even-slice.t()")
     ops.add_(dy, dx.t())
     assert_bitexact(dy.numpy(), orc.binary(ADD, dtype, y, xt, 1.0), "y.add_(x.t())")
 
