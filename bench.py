@@ -28,7 +28,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,gemm32,linear,bmm,reduce,reduce_all,softmax,nn,mlp}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,gemm,gemm32,linear,bmm,reduce,reduce_all,softmax,nn,mlp,odd}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -841,7 +841,11 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              each operator: layer norm forward and backward [8192, 4096],
              dropout p = 0.1 and its backward, embedding of 8192 indices into
              [32000, 4096] and its dense gradient, nll_loss over
-             [8192, 32000] and its backward."""
+             [8192, 32000] and its backward;
+    odd:     products whose operands the matrix cores cannot read in place,
+             repacked: ten bf16 mm 2047^3 and five bf16 [2048, 4096] x
+             [4096, 50257]; then binary ops with transposed inputs, fp32 and
+             bf16 4096^2, ten x.t() + y and ten x.t() * y.t() each."""
     import ctypes as C
     if what == "traffic":
         a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
@@ -945,6 +949,26 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                 ops.nll_loss(logp, tgt, None, 1)
                 ops.nll_loss_backward(one, logp, tgt, None, 1, -100, total)
             del x, dy, w, b, mean, rstd, mask, table, logp, total
+    elif what == "odd":
+        g = np.random.default_rng(3)
+
+        def put(shape, dtype):
+            d = dev.from_numpy(g.standard_normal(shape, dtype=np.float32) * np.float32(0.05))
+            return d if dtype == F32 else ops.to(d, dtype)
+        a, b = put((2047, 2047), BF16), put((2047, 2047), BF16)
+        for _ in range(10):
+            ops.mm(a, b)
+        h, w = put((2048, 4096), BF16), put((4096, 50257), BF16)
+        for _ in range(5):
+            ops.mm(h, w)
+        del a, b, h, w
+        for dtype in (F32, BF16):
+            x, y = put((4096, 4096), dtype), put((4096, 4096), dtype)
+            for _ in range(10):
+                ops.add(x.t(), y)
+            for _ in range(10):
+                ops.mul(x.t(), y.t())
+            del x, y
     elif what == "mlp":
         wl = importlib.import_module("tensorplay-mlu_amd.workloads")
         ws, bs = wl.MLP.host_init(4096, 4, 4096, 1000, seed=0)
@@ -971,7 +995,7 @@ def main() -> int:
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "linear", "bmm", "reduce", "reduce_all",
-                                         "softmax", "nn", "mlp"],
+                                         "softmax", "nn", "mlp", "odd"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:

@@ -1085,10 +1085,48 @@ constexpr double kRepackMinMacs = double(int64_t(1) << 22);
 
 void check_status(int status) { TP_AMD_CHECK(status == 0, last_error()); }
 
+// A K-major source in one pass: dst row q (of bs x rows) = the source row
+// (b, r) = (q / rows, q % rows) at src + b stride + r ld, elements 0..k, then
+// zeros to kp.  A thread writes one 16-byte packet (kp is a whole number of
+// them) from element loads, which are unaligned when ld or k is odd.
+constexpr int kRepackBlock = 256;
+
+template <typename S>
+__global__ __launch_bounds__(kRepackBlock) void repack_rows_kernel(S* __restrict__ dst, const S* __restrict__ src,
+                                                                   int64_t total, int64_t rows, int64_t ld,
+                                                                   int64_t stride, int64_t k, int64_t kp) {
+    constexpr int N = 16 / sizeof(S);
+    const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * kRepackBlock + threadIdx.x) * N;
+    if (j0 >= kp) return;
+    for (int64_t q = blockIdx.y; q < total; q += gridDim.y) {
+        const S* row = src + (q / rows) * stride + (q % rows) * ld;
+        S v[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) v[e] = j0 + e < k ? row[j0 + e] : S{};
+        uint4 w;
+        __builtin_memcpy(&w, v, 16);
+        *reinterpret_cast<uint4*>(dst + q * kp + j0) = w;
+    }
+}
+
 // x logical [bs][rows][k] (element (b, r, j) at x + b stride + r ld + j when
 // K-major, + j ld + r otherwise) -> ws [bs][rows][kp], columns k..kp zero.
-void repack_kmajor(int device, int esize, const void* x, int64_t ld, int64_t stride, bool kmajor,
-                   int64_t bs, int64_t rows, int64_t k, int64_t kp, void* ws) {
+// K-major sources take repack_rows_kernel; the others the transpose copy and
+// a fill of the padding.
+template <typename S>
+void repack_kmajor(int device, const void* x, int64_t ld, int64_t stride, bool kmajor, int64_t bs,
+                   int64_t rows, int64_t k, int64_t kp, void* ws, hipStream_t stream) {
+    constexpr int esize = sizeof(S);
+    if (kmajor) {
+        constexpr int N = 16 / esize;
+        const int64_t total = bs * rows;
+        const dim3 grid(static_cast<unsigned>((kp / N + kRepackBlock - 1) / kRepackBlock),
+                        static_cast<unsigned>(std::min<int64_t>(total, 65535)));
+        repack_rows_kernel<S><<<grid, kRepackBlock, 0, stream>>>(static_cast<S*>(ws), static_cast<const S*>(x),
+                                                                 total, rows, ld, stride, k, kp);
+        TP_AMD_HIP_CHECK(hipGetLastError());
+        return;
+    }
     const int64_t sizes[3] = {bs, rows, k};
     const int64_t dst[3] = {rows * kp, kp, 1};
     const int64_t src[3] = {stride, kmajor ? ld : 1, kmajor ? 1 : ld};
@@ -1118,7 +1156,8 @@ void launch_repacked(const GemmArgs& p, hipStream_t stream) {
     GemmArgs q = p;
     q.k = kp;
     if (fix_a) {
-        repack_kmajor(device, E, p.a, p.lda, p.stride_a, !p.trans_a, bs_a, p.m, p.k, kp, ws.get());
+        repack_kmajor<typename Elem<T>::storage>(device, p.a, p.lda, p.stride_a, !p.trans_a, bs_a, p.m, p.k, kp,
+                                                 ws.get(), stream);
         q.a = ws.get();
         q.lda = kp;
         q.stride_a = p.stride_a == 0 ? 0 : p.m * kp;
@@ -1126,7 +1165,8 @@ void launch_repacked(const GemmArgs& p, hipStream_t stream) {
     }
     if (fix_b) {
         void* wb = static_cast<char*>(ws.get()) + off_b;
-        repack_kmajor(device, E, p.b, p.ldb, p.stride_b, p.trans_b, bs_b, p.n, p.k, kp, wb);
+        repack_kmajor<typename Elem<T>::storage>(device, p.b, p.ldb, p.stride_b, p.trans_b, bs_b, p.n, p.k, kp, wb,
+                                                 stream);
         q.b = wb;
         q.ldb = kp;
         q.stride_b = p.stride_b == 0 ? 0 : p.n * kp;
