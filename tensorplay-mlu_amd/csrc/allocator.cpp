@@ -12,7 +12,7 @@ namespace tp_amd {
 namespace {
 
 void* hip_acquire(int device, size_t nbytes, void*) {
-    DeviceGuard guard(device);
+    const OnDevice scope(device);
     void* ptr = nullptr;
     const hipError_t status = hipMalloc(&ptr, nbytes);
     if (status == hipErrorOutOfMemory) {
@@ -24,7 +24,7 @@ void* hip_acquire(int device, size_t nbytes, void*) {
 }
 
 void hip_release(int device, void* ptr, void*) {
-    DeviceGuard guard(device);
+    const OnDevice scope(device);
     (void)hipFree(ptr);
 }
 
@@ -118,9 +118,9 @@ size_t tp_amd_block_size(void* ctx) {
 
 int tp_mlu_init(void) {
     const int status = guarded([&] {
-        // Make the runtime usable and create the streams up front, so the
+        // Open every GPU's slot (its stream and properties) up front, so the
         // first operator does not pay for it.
-        for (int d = 0; d < device_count(); ++d) (void)stream(d);
+        open_all_devices();
     });
     if (status != TP_AMD_OK) return 1;
     // Built with the TensorPlay adapter (csrc/tensorplay/), the operators

@@ -479,8 +479,8 @@ int tp_amd_launch_fill(int device, int elem_size, const void* value, int ndim,
                        const int64_t* sizes, void* dst, const int64_t* dst_strides) {
     return guarded([&] {
         TP_AMD_CHECK(value != nullptr, "tp_amd_launch_fill: null value");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         switch (elem_size) {
             case 1: fill_typed<uint8_t>(index, value, ndim, sizes, dst, dst_strides); break;
             case 2: fill_typed<uint16_t>(index, value, ndim, sizes, dst, dst_strides); break;
@@ -496,8 +496,8 @@ int tp_amd_launch_cast(int device, int src_dtype, int dst_dtype, int64_t n, cons
     return guarded([&] {
         TP_AMD_CHECK(n >= 0, "negative element count");
         if (n == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         switch (src_dtype) {
             case TP_AMD_FLOAT32: cast_from<F32>(index, dst_dtype, n, src, dst); break;
             case TP_AMD_FLOAT16: cast_from<F16>(index, dst_dtype, n, src, dst); break;
@@ -518,8 +518,8 @@ int tp_amd_launch_strided_copy(int device, int elem_size, int ndim, const int64_
                                void* dst, const int64_t* dst_strides, const void* src,
                                const int64_t* src_strides) {
     return guarded([&] {
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         const int64_t* s[2] = {dst_strides, src_strides};
         const Layout<2> l = coalesce<2>(ndim, sizes, s);
         const int64_t n = l.numel();

@@ -590,8 +590,8 @@ int tp_amd_launch_binary(int device, int op, int dtype, int ndim, const int64_t*
                          const int64_t* b_strides, void* out, const int64_t* out_strides,
                          float alpha) {
     return guarded([&] {
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_FLOAT(dtype, T, {
             switch (op) {
                 case TP_AMD_BINARY_ADD:
@@ -617,8 +617,8 @@ int tp_amd_launch_affine(int device, int dtype, int64_t n, const void* x, float 
     return guarded([&] {
         TP_AMD_CHECK(n >= 0, "negative element count");
         if (n == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_FLOAT(dtype, T,
                               launch_flat<T, 1>(index, x, nullptr, y, n, AffineFn{alpha, beta}));
     });
@@ -627,8 +627,8 @@ int tp_amd_launch_affine(int device, int dtype, int64_t n, const void* x, float 
 int tp_amd_launch_unary(int device, int op, int dtype, int ndim, const int64_t* sizes,
                         const void* x, const int64_t* x_strides, void* y, float param) {
     return guarded([&] {
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_FLOAT(dtype, T,
                               unary_dispatch<T>(index, op, ndim, sizes, x, x_strides, y, param));
     });
@@ -640,8 +640,8 @@ int tp_amd_launch_activation_backward(int device, int op, int dtype, int64_t n,
     return guarded([&] {
         TP_AMD_CHECK(n >= 0, "negative element count");
         if (n == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_FLOAT(dtype, T,
                               backward_dispatch<T>(index, op, n, grad, saved, dx, param));
     });

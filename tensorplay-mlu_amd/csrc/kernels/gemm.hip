@@ -141,8 +141,8 @@ int tp_amd_launch_gemm(int device, int dtype, int64_t batch, int64_t m, int64_t 
         TP_AMD_CHECK(lda >= (trans_a ? m : k) || k == 0, "lda too small");
         TP_AMD_CHECK(ldb >= (trans_b ? k : n) || k == 0, "ldb too small");
         TP_AMD_CHECK(ldc >= n, "ldc too small");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         GemmArgs p{};
         p.batch = batch;
         p.m = m;

@@ -1454,8 +1454,8 @@ int tp_amd_launch_layer_norm(int device, int dtype, int64_t rows, int64_t dim, c
         TP_AMD_CHECK(rows >= 0 && dim > 0, "layer_norm: bad extent");
         if (rows == 0) return;
         TP_AMD_CHECK(rows <= 0x7fffffff, "layer_norm: too many rows");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_NN(dtype, T, layer_norm_typed<T>(index, rows, dim, x, weight, bias, y, mean, rstd,
                                                          static_cast<float>(eps)));
     });
@@ -1467,8 +1467,8 @@ int tp_amd_launch_layer_norm_backward(int device, int dtype, int64_t rows, int64
                                       void* dbias) {
     return guarded([&] {
         TP_AMD_CHECK(rows >= 0 && dim > 0, "layer_norm_backward: bad extent");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         if (rows == 0) {
             // No rows: the parameter gradients are zero.
             TP_AMD_DISPATCH_NN(dtype, T, {
@@ -1496,8 +1496,8 @@ int tp_amd_launch_dropout(int device, int dtype, int64_t n, const void* x, doubl
     return guarded([&] {
         TP_AMD_CHECK(n >= 0 && p >= 0.0 && p < 1.0, "dropout: need 0 <= p < 1");
         if (n == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         const float scale = static_cast<float>(1.0 / (1.0 - p));
         // p 2^24 is exact in double; a 24-bit uniform u 2^-24 is >= p exactly
         // when u >= ceil(p 2^24) (at most 2^24, which keeps nothing).
@@ -1519,8 +1519,8 @@ int tp_amd_launch_dropout_backward(int device, int dtype, int64_t n, const void*
     return guarded([&] {
         TP_AMD_CHECK(n >= 0, "dropout_backward: negative extent");
         if (n == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_DISPATCH_NN(dtype, T, {
             constexpr int N = Packet<T>::N;
             const bool vec = aligned16(grad) && aligned16(out) && reinterpret_cast<uintptr_t>(mask) % N == 0;
@@ -1537,8 +1537,8 @@ int tp_amd_launch_embedding(int device, int dtype, int64_t num_weights, int64_t 
     return guarded([&] {
         TP_AMD_CHECK(num_weights >= 0 && dim >= 0 && n >= 0, "embedding: negative extent");
         if (n == 0 || dim == 0) return;
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         const int64_t blocks = blocks_for(n, kBlock / kWave);
         TP_AMD_DISPATCH_NN(dtype, T, {
             const bool vec = dim % Packet<T>::N == 0 && aligned16(weight) && aligned16(out);
@@ -1567,8 +1567,8 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
         if (num_weights == 0 || dim == 0) return;
         TP_AMD_CHECK(n < 0x7fffffff && num_weights < 0x7fffffff,
                      "embedding_backward: at most 2^31 - 2 samples and table rows");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         hipStream_t st = stream(index);
         // The plan by row ranges (about one block per CU, at most kRangeRows
         // rows each) when its blocks' index reads stay under kRangeReadCap;
@@ -1653,8 +1653,8 @@ int tp_amd_launch_nll_loss(int device, int dtype, int64_t n, int64_t classes, co
     return guarded([&] {
         TP_AMD_CHECK(n > 0 && classes > 0, "nll_loss: empty input");
         TP_AMD_CHECK(reduction >= 0 && reduction <= 2, "nll_loss: reduction must be 0, 1 or 2");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         hipStream_t st = stream(index);
         const int64_t blocks = blocks_for(n, kBlock);
         TP_AMD_DISPATCH_NN(dtype, T, {
@@ -1678,8 +1678,8 @@ int tp_amd_launch_nll_loss_backward(int device, int dtype, int64_t n, int64_t cl
     return guarded([&] {
         TP_AMD_CHECK(n > 0 && classes > 0, "nll_loss_backward: empty input");
         TP_AMD_CHECK(reduction >= 0 && reduction <= 2, "nll_loss_backward: reduction must be 0, 1 or 2");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         const int64_t blocks = blocks_for(n * classes, kBlock);
         TP_AMD_DISPATCH_NN(dtype, T, {
             constexpr int N = Packet<T>::N;

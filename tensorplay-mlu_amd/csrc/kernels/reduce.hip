@@ -795,8 +795,8 @@ int launch_reduce(int device, int op, int dtype, int64_t outer, int64_t r, int64
         TP_AMD_CHECK(outer >= 0 && r >= 0 && inner >= 0, "negative reduce extent");
         if (outer == 0 || inner == 0) return;
         TP_AMD_CHECK(r > 0, "reduce over an empty axis: the caller fills the result");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         const Scratch scratch = no_alloc ? static_scratch(index) : Scratch{};
         switch (dtype) {
             case TP_AMD_FLOAT32: reduce_dispatch_op<float>(index, op, outer, r, inner, x, out, scratch); break;

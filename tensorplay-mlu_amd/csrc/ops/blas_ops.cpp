@@ -1,11 +1,37 @@
-// Matrix products: the C entry points for the reference's 5 BLAS
-// registrations (tensorplay_mlu/csrc/BlasKernels.cpp:32-422): mm, bmm,
-// addmm, linear, matmul, over the gfx950 GEMM kernels.  A transposed view of
-// a row-major matrix is read in place (as_operand, :38-54); addmm's bias is
-// read by the GEMM epilogue directly instead of being copied into the output
-// first (:318-324) -- the same beta * bias + alpha * product.
+// Matrix products: mm, bmm, addmm, linear and matmul (the five BLAS
+// registrations of tensorplay_mlu/csrc/BlasKernels.cpp:416-422).
+//
+// Every entry point only validates its operands and states its product as
+//
+//     out[b] (m x n) = alpha * L[b] (m x k) . R[b] (k x n) + beta * addend
+//
+// over a batch shape (empty for a plain product).  One planner (Product)
+// then decides how the gfx950 GEMM kernels address each side:
+//   * a side whose matrix is row-major, or the transpose of a row-major
+//     matrix, with any leading dimension, is read where it lies; its batch
+//     dimensions must collapse to one stride (0 for a broadcast side);
+//   * anything else -- stride-0 matrix axes, unmergeable batch strides --
+//     is first copied into a dense stack;
+//   * a left side whose batch continues its rows, against a broadcast right
+//     side, folds the batch into the rows: one product of B*m rows (the
+//     [..., M, K] @ [K, N] matmul case, and linear on a 3-D input);
+// and launches one GEMM.  The result is allocated directly in the shape the
+// caller sees (vector operands drop their unit axis, linear keeps the
+// input's leading dimensions), which is the dense [B, m, n] stack the GEMM
+// writes.
+//
+// Semantics kept from the reference: which operands decline to the host
+// (:244-248 and each kernel's first test), the shape errors, an inner size
+// of 0 giving zeros or beta * bias (:265-268, :277-280, :326-329), addmm's
+// beta * bias + alpha * product with the bias ignored when beta is 0
+// (:318-324), linear as a product over the flattened rows with W read
+// transposed (:338-356), and matmul's 1-D promotion and batch broadcasting
+// (:360-412).  Where the reference densifies (reshape_dense, the expanded
+// batch of the general matmul case) this planner reads in place whenever
+// the kernels can; the values are the same dot products either way.
 
-#include <numeric>
+#include <utility>
+#include <vector>
 
 #include "tensor.h"
 #include "tp_amd_kernels.h"
@@ -15,263 +41,276 @@ using namespace tp_amd;
 
 namespace {
 
-// A matrix operand as the GEMM reads it: the stored row-major matrix, its
-// leading dimension, batch stride, and whether the product reads it
-// transposed (Operand / as_operand, :32-54).
-struct Operand {
-    MaybeOwned storage;
-    bool transposed = false;
-    int64_t ld = 0;
+// How the kernels address one side: matrix b starts at data + b *
+// batch_stride elements; element (i, j) sits at i * ld + j, or at j * ld + i
+// when the side is stored as the transpose of a row-major matrix.
+struct MatrixRead {
+    const void* data = nullptr;
+    int64_t ld = 1;
     int64_t batch_stride = 0;
+    bool transposed = false;
 };
 
-Operand as_operand(const TensorRef& t) {
-    const int nd = t.ndim;
-    const int64_t r = t.sizes[nd - 2], c = t.sizes[nd - 1];
-    const int64_t s_r = t.strides[nd - 2], s_c = t.strides[nd - 1];
-    const bool batch_ok = nd == 2 || t.strides[0] == r * c || t.sizes[0] == 1;
-    const int64_t bstride = nd == 3 && t.sizes[0] > 1 ? r * c : 0;
-    Operand op;
-    if (batch_ok && (s_c == 1 || c == 1) && (s_r == c || r == 1)) {
-        op.storage.ref = t;
-        op.storage.ref.ctx = nullptr;
-        op.transposed = false;
-        op.ld = c;
-        op.batch_stride = bstride;
-        return op;
+// The matrix axes (the last two) of ``t`` as a MatrixRead, or false when
+// neither axis is unit-stride with the other spanning at least a full line.
+bool matrix_axes_in_place(const TensorRef& t, MatrixRead& read) {
+    const int64_t rows = t.sizes[t.ndim - 2], cols = t.sizes[t.ndim - 1];
+    const int64_t row_step = t.strides[t.ndim - 2], col_step = t.strides[t.ndim - 1];
+    read.data = t.data;
+    if ((cols == 1 || col_step == 1) && (rows == 1 || row_step >= cols)) {
+        read.transposed = false;
+        read.ld = rows == 1 ? cols : row_step;
+        return true;
     }
-    if (batch_ok && (s_r == 1 || r == 1) && (s_c == r || c == 1)) {
-        op.storage.ref = t;
-        op.storage.ref.ctx = nullptr;
-        op.transposed = true;
-        op.ld = r;
-        op.batch_stride = bstride;
-        return op;
+    if ((rows == 1 || row_step == 1) && (cols == 1 || col_step >= rows)) {
+        read.transposed = true;
+        read.ld = cols == 1 ? rows : col_step;
+        return true;
     }
-    op.storage = contiguous_on_device(t);
-    op.transposed = false;
-    op.ld = c;
-    op.batch_stride = bstride;
-    return op;
+    return false;
 }
 
-// out (dense [.., M, N]) = alpha * a @ b + beta * cin (gemm, :202-242).
-// ``cin`` null means beta is 0.
-void gemm(const TensorRef& a, const TensorRef& b, const TensorRef& out, float alpha, float beta,
-          const TensorRef* cin) {
-    Operand oa = as_operand(a), ob = as_operand(b);
-    const bool batched = out.ndim == 3;
-    const int64_t B = batched ? out.sizes[0] : 1;
-    const int64_t M = out.sizes[out.ndim - 2], N = out.sizes[out.ndim - 1];
-    const int64_t K = a.sizes[a.ndim - 1];
-    const void* cptr = nullptr;
-    int64_t crs = 0, ccs = 0, csb = 0;
-    if (cin != nullptr && beta != 0.0f) {
-        cptr = cin->data;
-        crs = cin->strides[cin->ndim - 2];
-        ccs = cin->strides[cin->ndim - 1];
-        csb = cin->ndim == 3 ? cin->strides[0] : 0;
-    } else {
-        beta = 0.0f;
+// The first ``nbatch`` axes of ``t`` walked as one flattened index: true with
+// the single element stride that index steps by, or false when the axes do
+// not merge (a broadcast axis next to a stored one, or a gap).
+bool batch_axes_merge(const TensorRef& t, int nbatch, int64_t& step) {
+    bool seen = false;
+    int64_t next = 0;  // the stride the next outer non-unit axis must have
+    step = 0;
+    for (int d = nbatch - 1; d >= 0; --d) {
+        if (t.sizes[d] == 1) continue;
+        if (!seen) {
+            step = t.strides[d];
+            next = step * t.sizes[d];
+            seen = true;
+        } else if (t.strides[d] != next) {
+            return false;
+        } else {
+            next *= t.sizes[d];
+        }
     }
-    const int st = tp_amd_launch_gemm(out.device, out.dtype, B, M, N, K, alpha,
-                                      oa.storage.ref.data, oa.ld, oa.batch_stride,
-                                      oa.transposed ? 1 : 0, ob.storage.ref.data, ob.ld,
-                                      ob.batch_stride, ob.transposed ? 1 : 0, beta, cptr, crs, ccs,
-                                      csb, out.data, N, batched ? M * N : 0);
-    TP_AMD_CHECK(st == TP_AMD_OK, last_error());
+    return true;
 }
 
-bool native_pair(const TensorRef& a, const TensorRef& b) {
-    return on_device(a) && on_device(b) && is_native_float(a.dtype) && a.dtype == b.dtype &&
-           a.device == b.device;
+Sizes with_matrix(Sizes shape, int64_t rows, int64_t cols) {
+    shape.push_back(rows);
+    shape.push_back(cols);
+    return shape;
 }
 
-// A dense tensor's memory under a new contiguous shape (reshape_dense,
-// :251-259): a contiguous copy first when needed.
-MaybeOwned reshape_dense(const TensorRef& t, const Sizes& sizes) {
-    MaybeOwned c = contiguous_on_device(t);
-    c.ref = make_view(c.ref, sizes, contiguous_strides(sizes));
-    if (c.hold.ref().ctx != nullptr) c.ref.ctx = nullptr;
-    return c;
-}
+class Product {
+public:
+    // lhs [..., m, k] and rhs [..., k, n], both with at least two axes, inner
+    // sizes already checked equal; ``batch`` is their broadcast batch shape
+    // and ``result_shape`` the shape handed back (numel batch * m * n).
+    Product(const TensorRef& lhs, const TensorRef& rhs, Sizes batch, Sizes result_shape)
+        : lhs_(lhs), rhs_(rhs), batch_shape_(std::move(batch)), result_shape_(std::move(result_shape)) {
+        m_ = lhs.sizes[lhs.ndim - 2];
+        k_ = lhs.sizes[lhs.ndim - 1];
+        n_ = rhs.sizes[rhs.ndim - 1];
+        batch_ = 1;
+        for (int64_t d : batch_shape_) batch_ *= d;
+    }
 
-void zero(const TensorRef& t) { fill(t, scalar_of(0.0)); }
-
-Owned mm_native(const TensorRef& a, const TensorRef& b) {
-    const int64_t M = a.sizes[0], N = b.sizes[1];
-    Owned out = empty_on({M, N}, a.dtype, a.device);
-    if (numel(out.ref()) == 0) return out;
-    if (a.sizes[1] == 0) {
-        zero(out.ref());
+    // ``addend`` (beta != 0 only) is a 2-D view over all batch * m output
+    // rows: row r of it is added to output row r.
+    Owned run(float alpha, float beta, const TensorRef* addend) {
+        Owned out = empty_on(result_shape_, lhs_.dtype, lhs_.device);
+        if (numel(out.ref()) == 0) return out;
+        const TensorRef rows = make_view(out.ref(), {batch_ * m_, n_}, {n_, 1});
+        if (k_ == 0) {
+            no_terms(rows, beta, addend);
+            return out;
+        }
+        std::vector<Owned> copies;
+        const MatrixRead l = address(lhs_, m_, k_, copies);
+        const MatrixRead r = address(rhs_, k_, n_, copies);
+        // Fold the batch into the rows when the left stack's rows run on
+        // from one matrix to the next and the right side is shared.
+        const bool fold = batch_ > 1 && r.batch_stride == 0 && !l.transposed &&
+                          l.batch_stride == m_ * l.ld;
+        const int64_t nb = fold ? 1 : batch_, m = fold ? batch_ * m_ : m_;
+        const void* cin = nullptr;
+        int64_t cin_rs = 0, cin_cs = 0;
+        if (addend != nullptr && beta != 0.0f) {
+            cin = addend->data;
+            cin_rs = addend->strides[0];
+            cin_cs = addend->strides[1];
+        } else {
+            beta = 0.0f;
+        }
+        const int st = tp_amd_launch_gemm(
+            rows.device, rows.dtype, nb, m, n_, k_, alpha, l.data, l.ld, fold ? 0 : l.batch_stride,
+            l.transposed ? 1 : 0, r.data, r.ld, r.batch_stride, r.transposed ? 1 : 0, beta, cin, cin_rs,
+            cin_cs, m * cin_rs, rows.data, n_, m * n_);
+        TP_AMD_CHECK(st == TP_AMD_OK, last_error());
         return out;
     }
-    gemm(a, b, out.ref(), 1.0f, 0.0f, nullptr);
-    return out;
+
+private:
+    // An empty sum: every output element is 0, or beta * addend.
+    static void no_terms(const TensorRef& rows, float beta, const TensorRef* addend) {
+        if (addend == nullptr || beta == 0.0f) {
+            fill(rows, scalar_of(0.0));
+            return;
+        }
+        strided_copy(rows, *addend);
+        if (beta != 1.0f) {
+            const int st = tp_amd_launch_affine(rows.device, rows.dtype, numel(rows), rows.data, beta,
+                                                0.0f, rows.data);
+            TP_AMD_CHECK(st == TP_AMD_OK, last_error());
+        }
+    }
+
+    // One side as the kernels read it, copying it into ``copies`` when its
+    // layout cannot be addressed.  A side whose own batch axes are all 1 is
+    // shared by every matrix of the batch (stride 0), and only its one
+    // matrix is ever copied.
+    MatrixRead address(const TensorRef& side, int64_t rows, int64_t cols, std::vector<Owned>& copies) const {
+        const int own = side.ndim - 2;
+        bool shared = true;
+        for (int d = 0; d < own; ++d) shared = shared && side.sizes[d] == 1;
+        MatrixRead read;
+        if (shared) {
+            const TensorRef matrix = make_view(side, {rows, cols}, {side.strides[own], side.strides[own + 1]});
+            if (matrix_axes_in_place(matrix, read)) return read;
+            return dense_copy(matrix, {rows, cols}, copies);
+        }
+        const Sizes full = with_matrix(batch_shape_, rows, cols);
+        const TensorRef stack = expand_to(side, full);
+        const int nbatch = static_cast<int>(batch_shape_.size());
+        if (matrix_axes_in_place(stack, read) && batch_axes_merge(stack, nbatch, read.batch_stride)) {
+            return read;
+        }
+        MatrixRead packed = dense_copy(stack, full, copies);
+        packed.batch_stride = rows * cols;
+        return packed;
+    }
+
+    static MatrixRead dense_copy(const TensorRef& view, const Sizes& shape, std::vector<Owned>& copies) {
+        copies.push_back(empty_on(shape, view.dtype, view.device));
+        strided_copy(copies.back().ref(), view);
+        MatrixRead read;
+        read.data = copies.back().ref().data;
+        read.ld = shape.back();
+        return read;
+    }
+
+    TensorRef lhs_, rhs_;
+    Sizes batch_shape_, result_shape_;
+    int64_t batch_ = 1, m_ = 0, n_ = 0, k_ = 0;
+};
+
+// Both sides on one device in one of the three float dtypes the kernels
+// take; any other pairing runs on the host.
+bool device_float_pair(const TensorRef& a, const TensorRef& b) {
+    return on_device(a) && on_device(b) && a.device == b.device && a.dtype == b.dtype &&
+           is_native_float(a.dtype);
 }
 
-Owned bmm_native(const TensorRef& a, const TensorRef& b) {
-    const int64_t B = a.sizes[0], M = a.sizes[1], N = b.sizes[2];
-    Owned out = empty_on({B, M, N}, a.dtype, a.device);
-    if (numel(out.ref()) == 0) return out;
-    if (a.sizes[2] == 0) {
-        zero(out.ref());
-        return out;
-    }
-    gemm(a, b, out.ref(), 1.0f, 0.0f, nullptr);
-    return out;
+// A 1-D operand as a one-row ([1, k]) or one-column ([k, 1]) matrix view.
+TensorRef as_row(const TensorRef& v) {
+    return make_view(v, {1, v.sizes[0]}, {v.sizes[0] * v.strides[0], v.strides[0]});
+}
+TensorRef as_column(const TensorRef& v) { return make_view(v, {v.sizes[0], 1}, {v.strides[0], 1}); }
+
+TensorRef swap_last_two(const TensorRef& t) {
+    Sizes sizes = sizes_of(t), strides = strides_of(t);
+    std::swap(sizes[t.ndim - 2], sizes[t.ndim - 1]);
+    std::swap(strides[t.ndim - 2], strides[t.ndim - 1]);
+    return make_view(t, sizes, strides);
 }
 
 Owned mm_op(const TensorRef& self, const TensorRef& mat2) {
     check_view(self, "self");
     check_view(mat2, "mat2");
-    if (!native_pair(self, mat2) || self.ndim != 2 || mat2.ndim != 2) {
-        TP_AMD_DECLINE("mm operands have no device kernel");
+    if (!device_float_pair(self, mat2) || self.ndim != 2 || mat2.ndim != 2) {
+        TP_AMD_DECLINE("mm runs on the device for two 2-D float tensors of one dtype");
     }
-    TP_AMD_CHECK(self.sizes[1] == mat2.sizes[0], "mm: shapes ", self.sizes[0], "x",
-                 self.sizes[1], " and ", mat2.sizes[0], "x", mat2.sizes[1],
-                 " cannot be multiplied");
-    return mm_native(self, mat2);
+    TP_AMD_CHECK(self.sizes[1] == mat2.sizes[0], "mm: [", self.sizes[0], ", ", self.sizes[1],
+                 "] times [", mat2.sizes[0], ", ", mat2.sizes[1], "]: the inner sizes differ");
+    return Product(self, mat2, {}, {self.sizes[0], mat2.sizes[1]}).run(1.0f, 0.0f, nullptr);
 }
 
 Owned bmm_op(const TensorRef& self, const TensorRef& mat2) {
     check_view(self, "self");
     check_view(mat2, "mat2");
-    if (!native_pair(self, mat2) || self.ndim != 3 || mat2.ndim != 3) {
-        TP_AMD_DECLINE("bmm operands have no device kernel");
+    if (!device_float_pair(self, mat2) || self.ndim != 3 || mat2.ndim != 3) {
+        TP_AMD_DECLINE("bmm runs on the device for two 3-D float tensors of one dtype");
     }
-    TP_AMD_CHECK(self.sizes[0] == mat2.sizes[0] && self.sizes[2] == mat2.sizes[1],
-                 "bmm: batch or inner dimensions do not match");
-    return bmm_native(self, mat2);
+    TP_AMD_CHECK(self.sizes[0] == mat2.sizes[0], "bmm: ", self.sizes[0], " and ", mat2.sizes[0],
+                 " matrices in the two stacks");
+    TP_AMD_CHECK(self.sizes[2] == mat2.sizes[1], "bmm: inner sizes ", self.sizes[2], " and ",
+                 mat2.sizes[1], " differ");
+    const int64_t b = self.sizes[0];
+    return Product(self, mat2, {b}, {b, self.sizes[1], mat2.sizes[2]}).run(1.0f, 0.0f, nullptr);
 }
 
-// beta * self + alpha * mat1 @ mat2 (addmm_kernel, :306-334).
 Owned addmm_op(const TensorRef& self, const TensorRef& mat1, const TensorRef& mat2, double beta,
                double alpha) {
     check_view(self, "self");
     check_view(mat1, "mat1");
     check_view(mat2, "mat2");
-    if (!native_pair(mat1, mat2) || mat1.ndim != 2 || mat2.ndim != 2 || !on_device(self) ||
-        self.dtype != mat1.dtype || self.device != mat1.device) {
-        TP_AMD_DECLINE("addmm operands have no device kernel");
+    if (!device_float_pair(mat1, mat2) || mat1.ndim != 2 || mat2.ndim != 2 ||
+        !device_float_pair(self, mat1)) {
+        TP_AMD_DECLINE("addmm runs on the device when bias and both matrices share a float dtype and device");
     }
-    TP_AMD_CHECK(mat1.sizes[1] == mat2.sizes[0], "addmm: shapes cannot be multiplied");
-    const int64_t M = mat1.sizes[0], N = mat2.sizes[1];
-    Owned out = empty_on({M, N}, mat1.dtype, mat1.device);
-    if (numel(out.ref()) == 0) return out;
-    const float b = static_cast<float>(beta), a = static_cast<float>(alpha);
-    const TensorRef bias = expand_to(self, {M, N});
-    if (mat1.sizes[1] == 0) {
-        if (b == 0.0f) {
-            zero(out.ref());
-        } else {
-            strided_copy(out.ref(), bias);
-            if (b != 1.0f) {
-                const int st = tp_amd_launch_affine(out.ref().device, out.ref().dtype,
-                                                    numel(out.ref()), out.ref().data, b, 0.0f,
-                                                    out.ref().data);
-                TP_AMD_CHECK(st == TP_AMD_OK, last_error());
-            }
-        }
-        return out;
-    }
-    gemm(mat1, mat2, out.ref(), a, b, b != 0.0f ? &bias : nullptr);
-    return out;
+    TP_AMD_CHECK(mat1.sizes[1] == mat2.sizes[0], "addmm: mat1 has ", mat1.sizes[1],
+                 " columns but mat2 has ", mat2.sizes[0], " rows");
+    const int64_t m = mat1.sizes[0], n = mat2.sizes[1];
+    Product product(mat1, mat2, {}, {m, n});
+    // beta is applied in float32; a beta that rounds to 0 leaves the bias
+    // unread (its shape is not even checked), as the reference's does.
+    const float a = static_cast<float>(alpha), b = static_cast<float>(beta);
+    if (b == 0.0f) return product.run(a, 0.0f, nullptr);
+    const TensorRef bias = expand_to(self, {m, n});
+    return product.run(a, b, &bias);
 }
 
-TensorRef transpose2d(const TensorRef& t) {
-    return make_view(t, {t.sizes[1], t.sizes[0]}, {t.strides[1], t.strides[0]});
-}
-
-// input [..., K] @ weight [N, K].t() (+ bias [N]) (linear_kernel, :338-356).
 Owned linear_op(const TensorRef& input, const TensorRef& weight, const TensorRef* bias) {
     check_view(input, "input");
     check_view(weight, "weight");
-    const bool has_bias = bias != nullptr;
-    if (has_bias) check_view(*bias, "bias");
-    if (!native_pair(input, weight) || input.ndim == 0 || weight.ndim != 2 ||
-        (has_bias && (!on_device(*bias) || bias->dtype != input.dtype))) {
-        TP_AMD_DECLINE("linear operands have no device kernel");
+    if (bias != nullptr) check_view(*bias, "bias");
+    if (!device_float_pair(input, weight) || input.ndim == 0 || weight.ndim != 2 ||
+        (bias != nullptr && !device_float_pair(*bias, input))) {
+        TP_AMD_DECLINE("linear runs on the device when input, weight and bias share a float dtype and device");
     }
-    const int64_t K = weight.sizes[1], N = weight.sizes[0];
-    TP_AMD_CHECK(input.sizes[input.ndim - 1] == K, "linear: mat1 and mat2 shapes cannot be "
-                 "multiplied (", input.sizes[input.ndim - 1], " and ", K, ")");
-    const int64_t rows = numel(input) / std::max<int64_t>(K, 1);
-    MaybeOwned in2 = reshape_dense(input, {rows, K});
-    const TensorRef wt = transpose2d(weight);
-    Owned out = has_bias ? addmm_op(*bias, in2.ref, wt, 1.0, 1.0) : mm_op(in2.ref, wt);
-    Sizes shape = sizes_of(input);
-    shape.back() = N;
-    TensorRef view = make_view(out.ref(), shape, contiguous_strides(shape));
-    view.ctx = out.ref().ctx;
-    out.release();
-    return Owned(view);
+    const int64_t n = weight.sizes[0], k = weight.sizes[1];
+    TP_AMD_CHECK(input.sizes[input.ndim - 1] == k, "linear: input rows have ",
+                 input.sizes[input.ndim - 1], " features, the weight expects ", k);
+    // The rows of the product are every index of the input's leading axes.
+    Sizes result = sizes_of(input);
+    result.back() = n;
+    int64_t rows = 1;
+    for (int d = 0; d + 1 < input.ndim; ++d) rows *= input.sizes[d];
+    const TensorRef lhs = input.ndim == 1 ? as_row(input) : input;
+    const Sizes batch(lhs.sizes, lhs.sizes + lhs.ndim - 2);
+    Product product(lhs, swap_last_two(weight), batch, result);
+    if (bias == nullptr) return product.run(1.0f, 0.0f, nullptr);
+    const TensorRef addend = expand_to(*bias, {rows, n});
+    return product.run(1.0f, 1.0f, &addend);
 }
 
-Owned with_shape(Owned t, const Sizes& shape) {
-    TensorRef view = make_view(t.ref(), shape, contiguous_strides(shape));
-    view.ctx = t.ref().ctx;
-    t.release();
-    return Owned(view);
-}
-
-// matmul over broadcast batch dimensions (matmul_kernel, :360-412).
 Owned matmul_op(const TensorRef& self, const TensorRef& other) {
     check_view(self, "self");
     check_view(other, "other");
-    if (!native_pair(self, other) || self.ndim == 0 || other.ndim == 0) {
-        TP_AMD_DECLINE("matmul operands have no device kernel");
+    if (!device_float_pair(self, other) || self.ndim == 0 || other.ndim == 0) {
+        TP_AMD_DECLINE("matmul runs on the device for float tensors of one dtype with at least one axis");
     }
-    const int da = self.ndim, db = other.ndim;
-    if (da <= 2 && db <= 2) {
-        MaybeOwned a = da == 1 ? reshape_dense(self, {1, self.sizes[0]}) : MaybeOwned{self, Owned()};
-        MaybeOwned b = db == 1 ? reshape_dense(other, {other.sizes[0], 1}) : MaybeOwned{other, Owned()};
-        if (da != 1) a.ref.ctx = nullptr;
-        if (db != 1) b.ref.ctx = nullptr;
-        TP_AMD_CHECK(a.ref.sizes[1] == b.ref.sizes[0], "matmul: inner dimensions do not match");
-        Owned out = mm_native(a.ref, b.ref);
-        Sizes shape;
-        if (da == 2) shape.push_back(a.ref.sizes[0]);
-        if (db == 2) shape.push_back(b.ref.sizes[1]);
-        return with_shape(std::move(out), shape);
-    }
-    if (db <= 2 && da >= 3) {
-        // [..., M, K] @ [K, N]: fold the batch into the rows.
-        const int64_t K = self.sizes[da - 1];
-        const int64_t rows = numel(self) / std::max<int64_t>(K, 1);
-        MaybeOwned b = db == 1 ? reshape_dense(other, {other.sizes[0], 1}) : MaybeOwned{other, Owned()};
-        if (db != 1) b.ref.ctx = nullptr;
-        TP_AMD_CHECK(b.ref.sizes[0] == K, "matmul: inner dimensions do not match");
-        MaybeOwned a = reshape_dense(self, {rows, K});
-        Owned out = mm_native(a.ref, b.ref);
-        Sizes shape(self.sizes, self.sizes + da - 1);
-        if (db == 2) shape.push_back(b.ref.sizes[1]);
-        return with_shape(std::move(out), shape);
-    }
-    // General case: broadcast the batch dimensions, then one bmm.
-    MaybeOwned a = da == 1 ? reshape_dense(self, {1, self.sizes[0]}) : MaybeOwned{self, Owned()};
-    MaybeOwned b = db == 1 ? reshape_dense(other, {other.sizes[0], 1}) : MaybeOwned{other, Owned()};
-    if (da != 1) a.ref.ctx = nullptr;
-    if (db != 1) b.ref.ctx = nullptr;
-    const Sizes sa = sizes_of(a.ref), sb = sizes_of(b.ref);
-    const int64_t M = sa[sa.size() - 2], K = sa.back(), N = sb.back();
-    TP_AMD_CHECK(sb[sb.size() - 2] == K, "matmul: inner dimensions do not match");
-    const Sizes batch = broadcast_shape(Sizes(sa.begin(), sa.end() - 2), Sizes(sb.begin(), sb.end() - 2));
-    const int64_t B = std::accumulate(batch.begin(), batch.end(), int64_t(1),
-                                      std::multiplies<int64_t>());
-    auto expanded = [&](const TensorRef& t, int64_t r, int64_t c) {
-        Sizes shape = batch;
-        shape.push_back(r);
-        shape.push_back(c);
-        const TensorRef e = sizes_of(t) == shape ? t : expand_to(t, shape);
-        return reshape_dense(e, {B, r, c});
-    };
-    MaybeOwned ea = expanded(a.ref, M, K), eb = expanded(b.ref, K, N);
-    Owned out = bmm_native(ea.ref, eb.ref);
-    Sizes shape = batch;
-    if (da > 1) shape.push_back(M);
-    if (db > 1) shape.push_back(N);
-    return with_shape(std::move(out), shape);
+    // A vector on the left is one row, on the right one column; that unit
+    // axis is dropped from the result.
+    const TensorRef lhs = self.ndim == 1 ? as_row(self) : self;
+    const TensorRef rhs = other.ndim == 1 ? as_column(other) : other;
+    const int64_t m = lhs.sizes[lhs.ndim - 2], k = lhs.sizes[lhs.ndim - 1];
+    const int64_t n = rhs.sizes[rhs.ndim - 1];
+    TP_AMD_CHECK(rhs.sizes[rhs.ndim - 2] == k, "matmul: the left operand's last axis has ", k,
+                 " entries, the right operand's contracted axis ", rhs.sizes[rhs.ndim - 2]);
+    const Sizes batch = broadcast_shape(Sizes(lhs.sizes, lhs.sizes + lhs.ndim - 2),
+                                        Sizes(rhs.sizes, rhs.sizes + rhs.ndim - 2));
+    Sizes result = batch;
+    if (self.ndim > 1) result.push_back(m);
+    if (other.ndim > 1) result.push_back(n);
+    return Product(lhs, rhs, batch, result).run(1.0f, 0.0f, nullptr);
 }
 
 }  // namespace

@@ -45,16 +45,19 @@ bool is_contiguous(const TensorRef& t) {
     return true;
 }
 
+// Dense: the elements fill one gap-free block of memory in some axis order.
+// Sorting the non-unit axes by stride, each stride must equal the number of
+// elements the smaller-stride axes span.
 bool is_dense(const TensorRef& t) {
-    std::vector<int> order(t.ndim);
-    std::iota(order.begin(), order.end(), 0);
-    std::sort(order.begin(), order.end(),
-              [&](int a, int b) { return t.strides[a] < t.strides[b]; });
-    int64_t expected = 1;
-    for (int i : order) {
-        if (t.sizes[i] == 1) continue;
-        if (t.strides[i] != expected) return false;
-        expected *= t.sizes[i];
+    std::vector<std::pair<int64_t, int64_t>> axes;  // (stride, size) of the non-unit axes
+    for (int d = 0; d < t.ndim; ++d) {
+        if (t.sizes[d] != 1) axes.emplace_back(t.strides[d], t.sizes[d]);
+    }
+    std::sort(axes.begin(), axes.end());
+    int64_t span = 1;
+    for (const auto& [stride, size] : axes) {
+        if (stride != span) return false;
+        span *= size;
     }
     return true;
 }
@@ -182,27 +185,32 @@ int promote_types(int a, int b) {
     return width(a) >= width(b) ? a : b;
 }
 
+// A 0-d operand does not widen a dimensioned one whose category (bool <
+// integer < floating) is at least its own: float16 tensor + float64 0-d stays
+// float16, int32 tensor + int64 0-d stays int32, float tensor + int 0-d stays
+// float.  Otherwise (two dimensioned operands, two 0-d ones, or a 0-d one
+// of a higher category) the lattice above decides.
 int binary_result_dtype(int a_dtype, int a_ndim, int b_dtype, int b_ndim) {
     if (a_dtype == b_dtype) return a_dtype;
-    const bool a_scalar = a_ndim == 0, b_scalar = b_ndim == 0;
-    if (a_scalar != b_scalar) {
-        const int full = a_scalar ? b_dtype : a_dtype;
-        const int scalar = a_scalar ? a_dtype : b_dtype;
-        const bool same_kind = is_floating(full) == is_floating(scalar) &&
-                               (full == TP_AMD_BOOL) == (scalar == TP_AMD_BOOL);
-        if (same_kind || (is_floating(full) && !is_floating(scalar))) return full;
+    if ((a_ndim == 0) != (b_ndim == 0)) {
+        const int tensor = a_ndim == 0 ? b_dtype : a_dtype;
+        const int zero_d = a_ndim == 0 ? a_dtype : b_dtype;
+        if (category(tensor) >= category(zero_d)) return tensor;
     }
     return promote_types(a_dtype, b_dtype);
 }
 
+// Sizes aligned at the last axis; each pair must agree or one of them be 1,
+// and a missing leading axis counts as 1.
 Sizes broadcast_shape(const Sizes& a, const Sizes& b) {
-    const size_t n = std::max(a.size(), b.size());
-    Sizes out(n, 1);
-    for (size_t i = 0; i < n; ++i) {
-        const int64_t da = i < n - a.size() ? 1 : a[i - (n - a.size())];
-        const int64_t db = i < n - b.size() ? 1 : b[i - (n - b.size())];
-        TP_AMD_CHECK(da == db || da == 1 || db == 1, "shapes cannot be broadcast together");
-        out[i] = da == 1 ? db : da;
+    Sizes out(std::max(a.size(), b.size()));
+    auto ia = a.rbegin(), ib = b.rbegin();
+    for (auto o = out.rbegin(); o != out.rend(); ++o) {
+        const int64_t x = ia != a.rend() ? *ia++ : 1;
+        const int64_t y = ib != b.rend() ? *ib++ : 1;
+        TP_AMD_CHECK(x == y || x == 1 || y == 1, "broadcast: sizes ", x, " and ", y,
+                     " in one axis are unequal and neither is 1");
+        *o = x == 1 ? y : x;
     }
     return out;
 }

@@ -319,7 +319,7 @@ int tp_amd_timer_record(int device, void** marker) {
         if (device < 0 || device >= device_count()) return;
         hipEvent_t e = take_event();
         if (e == nullptr) return;
-        DeviceGuard guard(device);
+        const OnDevice scope(device);
         if (hipEventRecord(e, stream(device)) == hipSuccess) {
             *marker = e;
         } else {

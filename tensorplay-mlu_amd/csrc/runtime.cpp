@@ -15,11 +15,60 @@ namespace tp_amd {
 
 namespace {
 
-std::array<std::atomic<hipStream_t>, kMaxDevices> g_streams{};
-std::array<std::atomic<int>, kMaxDevices> g_cu_counts{};
-std::mutex g_stream_lock;
-
 thread_local std::string t_last_error;
+
+// One GPU's state.  ``opened`` guards the one-time set-up; a set-up that
+// throws leaves the slot closed and the next use tries again.
+struct DeviceSlot {
+    std::once_flag opened;
+    hipStream_t stream = nullptr;
+    int compute_units = 0;
+};
+
+// Every GPU the process sees, enumerated once.  The table is never
+// destroyed: streams stay valid until the process ends, also for work
+// queued from static destructors.
+class DeviceTable {
+public:
+    static DeviceTable& get() {
+        static DeviceTable* table = new DeviceTable();
+        return *table;
+    }
+
+    int size() const { return visible_; }
+
+    void require(int index) const {
+        if (index >= 0 && index < visible_) return;
+        throw Error(concat("GPU index ", index, " is out of range: this process sees ", visible_,
+                           visible_ == 1 ? " GPU" : " GPUs"));
+    }
+
+    const DeviceSlot& slot(int index) {
+        require(index);
+        DeviceSlot& s = slots_[index];
+        std::call_once(s.opened, [&] { open(index, s); });
+        return s;
+    }
+
+private:
+    DeviceTable() {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) {
+            (void)hipGetLastError();  // no driver or no GPU: an empty table
+            n = 0;
+        }
+        visible_ = std::min(n, kMaxDevices);
+    }
+
+    static void open(int index, DeviceSlot& s) {
+        const OnDevice scope(index);
+        TP_AMD_HIP_CHECK(hipDeviceGetAttribute(&s.compute_units, hipDeviceAttributeMultiprocessorCount, index));
+        TP_AMD_HIP_CHECK(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+    }
+
+    int visible_ = 0;
+    std::array<DeviceSlot, kMaxDevices> slots_;
+};
 
 }  // namespace
 
@@ -44,15 +93,11 @@ const char* dtype_name(int dtype) {
 }
 
 int device_count() noexcept {
-    static const int count = [] {
-        int n = 0;
-        if (hipGetDeviceCount(&n) != hipSuccess) {
-            (void)hipGetLastError();
-            return 0;
-        }
-        return n < kMaxDevices ? n : kMaxDevices;
-    }();
-    return count;
+    try {
+        return DeviceTable::get().size();
+    } catch (...) {
+        return 0;
+    }
 }
 
 int current_device() {
@@ -61,45 +106,41 @@ int current_device() {
     return index;
 }
 
-static void check_index(int index) {
-    const int count = device_count();
-    TP_AMD_CHECK(index >= 0 && index < count, "invalid device index ", index, " (", count,
-                 " device(s) visible)");
-}
-
 void set_device(int index) {
-    check_index(index);
+    DeviceTable::get().require(index);
     TP_AMD_HIP_CHECK(hipSetDevice(index));
 }
 
 int resolve_device(int index) {
-    TP_AMD_CHECK(device_count() > 0, "no GPU device is visible");
-    if (index < 0) index = current_device();
-    check_index(index);
-    return index;
+    DeviceTable& table = DeviceTable::get();
+    TP_AMD_CHECK(table.size() > 0, "no GPU is visible to this process");
+    const int resolved = index < 0 ? current_device() : index;
+    table.require(resolved);
+    return resolved;
 }
 
-DeviceGuard::DeviceGuard(int index) : previous_(current_device()), current_(index) {
-    if (current_ != previous_) set_device(current_);
+void open_all_devices() {
+    DeviceTable& table = DeviceTable::get();
+    for (int d = 0; d < table.size(); ++d) (void)table.slot(d);
 }
 
-DeviceGuard::~DeviceGuard() {
-    if (current_ != previous_) (void)hipSetDevice(previous_);
-}
-
-hipStream_t stream(int index) {
-    check_index(index);
-    hipStream_t s = g_streams[index].load(std::memory_order_acquire);
-    if (s != nullptr) return s;
-    std::lock_guard<std::mutex> lock(g_stream_lock);
-    s = g_streams[index].load(std::memory_order_relaxed);
-    if (s == nullptr) {
-        DeviceGuard guard(index);
-        TP_AMD_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-        g_streams[index].store(s, std::memory_order_release);
+OnDevice::OnDevice(int index) : index_(resolve_device(index)), restore_(-1) {
+    const int now = current_device();
+    if (now != index_) {
+        TP_AMD_HIP_CHECK(hipSetDevice(index_));
+        restore_ = now;
     }
-    return s;
 }
+
+OnDevice::~OnDevice() {
+    if (restore_ >= 0) (void)hipSetDevice(restore_);
+}
+
+hipStream_t OnDevice::stream() const { return DeviceTable::get().slot(index_).stream; }
+
+hipStream_t stream(int index) { return DeviceTable::get().slot(index).stream; }
+
+int cu_count(int index) { return DeviceTable::get().slot(index).compute_units; }
 
 namespace {
 
@@ -117,7 +158,7 @@ void refuse_while_recording(hipStream_t s, const char* what) {
 }  // namespace
 
 void synchronize(int index) {
-    DeviceGuard guard(index);
+    const OnDevice scope(index);
     refuse_while_recording(stream(index), "synchronisation");
     TP_AMD_HIP_CHECK(hipStreamSynchronize(stream(index)));
 }
@@ -273,7 +314,7 @@ void staged_to_host(char* dst, const char* src, size_t n, hipStream_t s, int ind
 
 void copy_to_device(void* device_dst, const void* host_src, size_t nbytes, int index) {
     if (nbytes == 0) return;
-    DeviceGuard guard(index);
+    const OnDevice scope(index);
     hipStream_t s = stream(index);
     refuse_while_recording(s, "a host-to-device copy");
     if (nbytes >= kStageFrom) {
@@ -286,7 +327,7 @@ void copy_to_device(void* device_dst, const void* host_src, size_t nbytes, int i
 
 void copy_to_host(void* host_dst, const void* device_src, size_t nbytes, int index) {
     if (nbytes == 0) return;
-    DeviceGuard guard(index);
+    const OnDevice scope(index);
     hipStream_t s = stream(index);
     refuse_while_recording(s, "a device-to-host copy");
     if (nbytes >= kStageFrom) {
@@ -299,18 +340,8 @@ void copy_to_host(void* host_dst, const void* device_src, size_t nbytes, int ind
 
 void copy_on_device(void* dst, const void* src, size_t nbytes, int index) {
     if (nbytes == 0 || dst == src) return;
-    DeviceGuard guard(index);
+    const OnDevice scope(index);
     TP_AMD_HIP_CHECK(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, stream(index)));
-}
-
-int cu_count(int index) {
-    check_index(index);
-    int n = g_cu_counts[index].load(std::memory_order_relaxed);
-    if (n == 0) {
-        TP_AMD_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, index));
-        g_cu_counts[index].store(n, std::memory_order_relaxed);
-    }
-    return n;
 }
 
 }  // namespace tp_amd
@@ -345,7 +376,7 @@ int tp_amd_mem_get_info(int index, size_t* free_bytes, size_t* total_bytes) {
     return guarded([&] {
         TP_AMD_CHECK(free_bytes != nullptr && total_bytes != nullptr,
                      "tp_amd_mem_get_info: null output");
-        DeviceGuard guard(resolve_device(index));
+        const OnDevice scope(index);
         TP_AMD_HIP_CHECK(hipMemGetInfo(free_bytes, total_bytes));
     });
 }
@@ -393,8 +424,8 @@ int tp_amd_event_create(void** event) {
 
 int tp_amd_event_record(void* event, int device) {
     return guarded([&] {
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         TP_AMD_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(event), stream(index)));
     });
 }

@@ -1,7 +1,10 @@
-// HIP device layer: device count, current device, one stream per device and
-// byte copies ordered on it.  MI355X-native replacement of the reference's
-// CNRT runtime glue (tensorplay_mlu/csrc/MLURuntime.h:54-96,
-// MLURuntime.cpp:34-136).
+// HIP device layer: which GPUs exist, one work stream per GPU, and byte
+// copies ordered on that stream.  It stands where the reference's CNRT glue
+// stands (tensorplay_mlu/csrc/MLURuntime.h:54-96): the same contract -- one
+// queue per device shared by every thread, host copies that return once the
+// bytes have landed, device copies that are only queued -- on a design of
+// its own: a table with one slot per GPU, filled once per GPU, and a scope
+// object that is the only way code here switches the current GPU.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,42 +17,51 @@ namespace tp_amd {
 
 constexpr int kMaxDevices = 64;
 
-// Visible devices, 0 when the driver or GPU is absent (MLURuntime.cpp:34-41).
+// GPUs this process sees (at most kMaxDevices; 0 without a driver or GPU).
 int device_count() noexcept;
 int current_device();
 void set_device(int index);
-// ``index`` itself when >= 0, else the current device; checked.
+// ``index`` when >= 0, else the current GPU; throws unless it names a
+// visible GPU.
 int resolve_device(int index);
 
-// Makes ``index`` current for the guard's lifetime (MLURuntime.cpp:73-79).
-class DeviceGuard {
+// Opens every visible GPU's slot now (tp_mlu_init), so the first operator
+// does not pay for stream creation.
+void open_all_devices();
+
+// For its lifetime, makes a GPU current (``index`` < 0: the current one) and
+// hands out that GPU's slot; the previous GPU is made current again at the
+// end of the scope, if the scope changed it.
+class OnDevice {
 public:
-    explicit DeviceGuard(int index);
-    ~DeviceGuard();
-    DeviceGuard(const DeviceGuard&) = delete;
-    DeviceGuard& operator=(const DeviceGuard&) = delete;
+    explicit OnDevice(int index);
+    ~OnDevice();
+    OnDevice(const OnDevice&) = delete;
+    OnDevice& operator=(const OnDevice&) = delete;
+
+    int index() const { return index_; }
+    hipStream_t stream() const;
 
 private:
-    int previous_;
-    int current_;
+    int index_;
+    int restore_;  // the GPU to make current again, or -1
 };
 
-// The single stream all work on ``index`` is issued to, created on first use
-// with default priority and no implicit synchronization with the null
-// stream (MLURuntime.cpp:81-93).
+// The stream every piece of work on GPU ``index`` is queued on: default
+// priority, no implicit synchronisation with the null stream.
 hipStream_t stream(int index);
 
-// Wait for the device's stream (MLURuntime.cpp:107-110).
+// Number of compute units of GPU ``index``, used to size grids.
+int cu_count(int index);
+
+// Wait until GPU ``index``'s stream has drained.
 void synchronize(int index);
 
 // Host copies return once the bytes have landed: the host side may be
-// pageable memory the caller frees right after (MLURuntime.cpp:112-129).
+// pageable memory the caller frees right after.
 void copy_to_device(void* device_dst, const void* host_src, size_t nbytes, int index);
 void copy_to_host(void* host_dst, const void* device_src, size_t nbytes, int index);
-// Ordered on the stream, asynchronous (MLURuntime.cpp:131-136).
+// Queued on the stream; returns at once.
 void copy_on_device(void* dst, const void* src, size_t nbytes, int index);
-
-// Number of compute units of ``index`` (cached), used to size grids.
-int cu_count(int index);
 
 }  // namespace tp_amd

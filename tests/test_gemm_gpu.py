@@ -133,6 +133,83 @@ def test_k_zero_and_empty(dev, ops, orc):
     assert np.array_equal(got, np.broadcast_to(np.arange(3, dtype=np.float32) * 2, (4, 3)))
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "bf16", "fp16"])
+def test_product_planner_layouts(dev, ops, orc, dtype):
+    """Layouts the product planner reads where they lie, or copies, with NaN
+    in every stored element outside the views (a read outside the view
+    shows up as NaN in the result)."""
+    d = lambda t: dev.from_numpy(t, dtype=dtype)  # noqa: E731
+    f = lambda t: orc.to_float(t, dtype)  # noqa: E731
+
+    def no_nan(got, what):
+        assert not np.isnan(f(got)).any(), f"{what}: read outside the view"
+
+    # mm on column slices: leading dimensions wider than the rows.
+    a = _padded(orc, (70, 40), 9, dtype, 1)
+    b = _padded(orc, (40, 33), 7, dtype, 2)
+    got = ops.mm(d(a)[:, :40], d(b)[:, :33]).numpy()
+    no_nan(got, "mm column slices")
+    check(orc, got, f(a)[:, :40] @ f(b)[:, :33], dtype, "mm column slices")
+    # bmm over every other matrix of a stack (batch stride 2 m k).
+    x = sample(orc, (8, 16, 24), dtype, 3)
+    y = sample(orc, (8, 24, 12), dtype, 4)
+    got = ops.bmm(d(x)[::2], d(y)[1::2]).numpy()
+    check(orc, got, f(x)[::2] @ f(y)[1::2], dtype, "bmm strided batch")
+    # [B, M, K] stored as transposes against a shared [K, N]: the batch does
+    # not fold into the rows, the shared side is read with batch stride 0.
+    xt = sample(orc, (5, 24, 16), dtype, 5)
+    w = _padded(orc, (24, 20), 4, dtype, 6)
+    got = ops.matmul(d(xt).transpose(1, 2), d(w)[:, :20]).numpy()
+    assert got.shape == (5, 16, 20)
+    no_nan(got, "matmul unfoldable batch")
+    check(orc, got, np.swapaxes(f(xt), 1, 2) @ f(w)[:, :20], dtype, "matmul unfoldable batch")
+    # [1, M, K] against [B, K, N] (left side shared), and [K] against [B, K, N].
+    l1 = sample(orc, (1, 16, 24), dtype, 7)
+    got = ops.matmul(d(l1), d(y)).numpy()
+    assert got.shape == (8, 16, 12)
+    check(orc, got, f(l1) @ f(y), dtype, "matmul shared left side")
+    v = sample(orc, (24,), dtype, 8)
+    got = ops.matmul(d(v), d(y)).numpy()
+    assert got.shape == (8, 12)
+    check(orc, got, f(v) @ f(y), dtype, "matmul vector @ stack")
+    # Batch axes that do not merge into one stride ([2, 3] from a permuted
+    # [3, 2] stack): copied dense first.
+    s = sample(orc, (3, 2, 16, 24), dtype, 9)
+    got = ops.matmul(d(s).permute(1, 0, 2, 3), d(y)[:6].view(2, 3, 24, 12)).numpy()
+    want = np.swapaxes(f(s), 0, 1) @ f(y)[:6].reshape(2, 3, 24, 12)
+    check(orc, got, want, dtype, "matmul unmergeable batch")
+    # linear on a permuted 3-D input with bias, and with an input whose rows
+    # are a column slice.
+    xin = sample(orc, (6, 4, 32), dtype, 10)
+    wt = sample(orc, (10, 32), dtype, 11)
+    bias = sample(orc, (10,), dtype, 12)
+    got = ops.linear(d(xin).permute(1, 0, 2), d(wt), d(bias)).numpy()
+    assert got.shape == (4, 6, 10)
+    want = np.swapaxes(f(xin), 0, 1) @ f(wt).T + f(bias)
+    check(orc, got, want, dtype, "linear permuted input")
+    xs = _padded(orc, (12, 32), 6, dtype, 13)
+    got = ops.linear(d(xs)[:, :32], d(wt), d(bias)).numpy()
+    no_nan(got, "linear column-slice input")
+    check(orc, got, f(xs)[:, :32] @ f(wt).T + f(bias), dtype, "linear column-slice input")
+
+
+def test_planner_empty_sums(dev, ops, orc):
+    """An inner size of 0 gives zeros, or beta * bias; linear keeps the
+    input's rows; addmm with beta = 0 never reads (or shape-checks) the
+    bias."""
+    z = lambda *s: dev.from_numpy(np.zeros(s, np.float32))  # noqa: E731
+    bias = np.array([1.0, -2.0, 3.0], np.float32)
+    got = ops.linear(z(4, 0), z(3, 0), dev.from_numpy(bias)).numpy()
+    assert np.array_equal(got, np.broadcast_to(bias, (4, 3)))
+    assert np.array_equal(ops.linear(z(2, 5, 0), z(3, 0)).numpy(), np.zeros((2, 5, 3), np.float32))
+    assert np.array_equal(ops.matmul(z(2, 4, 0), z(0, 3)).numpy(), np.zeros((2, 4, 3), np.float32))
+    a = np.random.default_rng(0).standard_normal((4, 6)).astype(np.float32)
+    b = np.random.default_rng(1).standard_normal((6, 3)).astype(np.float32)
+    odd_bias = dev.from_numpy(np.full((7,), np.nan, np.float32))
+    got = ops.addmm(odd_bias, dev.from_numpy(a), dev.from_numpy(b), beta=0.0, alpha=2.0).numpy()
+    check(orc, got, 2.0 * (a.astype(np.float64) @ b), F32, "addmm beta 0")
+
+
 # ---- full-size configs ------------------------------------------------------------
 
 
