@@ -598,9 +598,15 @@ __device__ __forceinline__ ColBlock col_block(int64_t tiles, int64_t slices, int
     return cb;
 }
 
-// (m, s) <- (m, s) merged with (m2, s2), each s a sum of exp(v - m).
+// The larger of a and b, NaN if either is (fmaxf returns the other operand
+// for a NaN, which would let a column whose only numbers are NaN and -inf
+// look empty and be skipped).
+__device__ __forceinline__ float max_keep_nan(float a, float b) { return (a > b || a != a) ? a : b; }
+
+// (m, s) <- (m, s) merged with (m2, s2), each s a sum of exp(v - m).  A NaN
+// maximum makes the merged sum NaN, so the column's outputs become NaN.
 __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
-    const float mn = fmaxf(m, m2);
+    const float mn = max_keep_nan(m, m2);
     if (mn == -INFINITY) return;
     s = (m == -INFINITY ? 0.0f : s * exp_fast(m - mn)) + (m2 == -INFINITY ? 0.0f : s2 * exp_fast(m2 - mn));
     m = mn;
@@ -630,9 +636,9 @@ __global__ __launch_bounds__(kColWaves * kWave) void softmax_cols_kernel(
 #pragma unroll
             for (int j = 0; j < kColBatch; ++j) {
                 if (d + j * kColWaves >= cb.d1) v[j] = -INFINITY;
-                bm = fmaxf(bm, v[j]);
+                bm = max_keep_nan(bm, v[j]);
             }
-            if (bm == -INFINITY) continue;
+            if (bm == -INFINITY) continue;  // only -inf and masked rows: nothing to add
             float bs = 0.0f;
 #pragma unroll
             for (int j = 0; j < kColBatch; ++j) bs += exp_fast(v[j] - bm);
@@ -960,8 +966,8 @@ int tp_amd_launch_softmax(int device, int log, int dtype, int64_t outer, int64_t
         TP_AMD_CHECK(outer >= 0 && dim >= 0 && inner >= 0, "negative softmax extent");
         if (outer == 0 || dim == 0 || inner == 0) return;
         TP_AMD_CHECK(outer <= 0x7fffffff, "softmax: too many rows");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         switch (dtype) {
             case TP_AMD_FLOAT32: softmax_typed<float>(index, log != 0, outer, dim, inner, x, y); break;
             case TP_AMD_BFLOAT16: softmax_typed<bf16_t>(index, log != 0, outer, dim, inner, x, y); break;
@@ -979,8 +985,8 @@ int tp_amd_launch_softmax_backward(int device, int log, int dtype, int64_t outer
         TP_AMD_CHECK(outer >= 0 && dim >= 0 && inner >= 0, "negative softmax extent");
         if (outer == 0 || dim == 0 || inner == 0) return;
         TP_AMD_CHECK(outer <= 0x7fffffff, "softmax: too many rows");
-        const int index = resolve_device(device);
-        DeviceGuard guard(index);
+        const OnDevice scope(device);
+        const int index = scope.index();
         switch (dtype) {
             case TP_AMD_FLOAT32:
                 softmax_backward_typed<float>(index, log != 0, outer, dim, inner, y, dy, dx);

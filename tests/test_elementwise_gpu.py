@@ -128,9 +128,9 @@ def test_transposed_operands_in_tiles(dev, ops, orc, dtype, rows, cols):
     """Binary ops with a transposed (column-major) operand into a row-major
     output, which run through LDS tiles of 64 x 64: either side transposed,
     both, a transposed operand with a broadcast row, a transposed slice of
-    a wider matrix (at odd and even offsets: 16-bit types with even sizes
-    and 4-byte aligned rows take 64 x 128 tiles of element pairs), and an
-    in-place update.  Bit-exact against the oracle."""
+    a wider matrix at an odd and at an even element offset (the same
+    kernel; the two offsets give different alignments of the tile loads),
+    and an in-place update.  Bit-exact against the oracle."""
     x = sample(orc, (cols, rows), dtype, 1)       # stored [cols][rows]; used as x.T
     y = sample(orc, (rows, cols), dtype, 2)
     z = sample(orc, (cols, rows), dtype, 3, 0.5, 2.0)

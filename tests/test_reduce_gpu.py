@@ -1,12 +1,14 @@
 """Reductions and softmax on the GPU against the CPU oracle: the
 reference's cases (tests/test_mlu.py:303-350) and config 3 of the benchmark
-at full size.  amax/amin are bit-exact; sums, means and softmax use the
-reference's norm-wise rule (tests/_check.py)."""
+at full size.  amax/amin are bit-exact; float32 sums and means use the
+reference's norm-wise rule, 16-bit ones also a per-element bound, and
+softmax and its backward per-element bounds (tests/_check.py)."""
 
 import numpy as np
 import pytest
 
-from _check import BF16, F16, F32, as_float, assert_bitexact, assert_normwise, assert_sum
+from _check import (BF16, F16, F32, as_float, assert_bitexact, assert_softmax, assert_softmax_backward,
+                    assert_sum)
 
 pytestmark = pytest.mark.gpu
 
@@ -49,19 +51,34 @@ def oracle_reduce(orc, op, dtype, x, dims, keepdim=False):
     return cur
 
 
+def check_sum(got, want, dtype, what, a, dims, mean=False, keepdim=False, mask=None):
+    """assert_sum with the per-element terms of a reduction of ``a`` over
+    ``dims`` (None or [] = all): the count of terms and the sum (or, for a
+    mean, the mean) of |x| per output; ``mask`` selects outputs."""
+    nd = a.ndim
+    axes = tuple(sorted(d % nd for d in (dims if dims else range(nd))))
+    n = int(np.prod([a.shape[d] for d in axes])) if axes else 1
+    x = np.abs(as_float(a, dtype).astype(np.float64)).sum(axis=axes, keepdims=keepdim)
+    x = x / n if mean else x
+    if mask is not None:
+        x = x[mask]
+    return assert_sum(got, want, dtype, what, n if mean else 1, x, n)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_reductions(dev, ops, orc, dtype):
     # a mean of 2 keeps every sum and mean well clear of the tolerance
     a = sample(orc, (6, 7, 8), dtype, mean=2.0)
     d = dev.from_numpy(a, dtype=dtype)
-    assert_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, "sum")
-    assert_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, "sum dim 1")
+    check_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, "sum", a, None)
+    check_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, "sum dim 1", a, [1])
     got = ops.sum_dim(d, (0, 2), keepdim=True).numpy()
     assert got.shape == (1, 7, 1)
-    assert_sum(got, oracle_reduce(orc, SUM, dtype, a, [0, 2], True), dtype, "sum (0, 2)")
-    assert_sum(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype, "mean", a.size)
-    assert_sum(ops.mean_dim(d, -1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [2]), dtype,
-               "mean dim -1", 8)
+    check_sum(got, oracle_reduce(orc, SUM, dtype, a, [0, 2], True), dtype, "sum (0, 2)", a, [0, 2],
+              keepdim=True)
+    check_sum(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype, "mean", a, None, True)
+    check_sum(ops.mean_dim(d, -1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [2]), dtype,
+              "mean dim -1", a, [2], True)
     for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
         for dims in ([0], [1], [-1], [0, 2], []):
             assert_bitexact(fn(d, dims).numpy(), oracle_reduce(orc, op, dtype, a, dims),
@@ -89,7 +106,7 @@ def test_column_reduction_row_chunks(dev, ops, orc, dtype, shape):
             else:
                 assert np.array_equal(np.isnan(orc.to_float(got, dtype)), np.isnan(orc.to_float(want, dtype)))
                 ok = ~np.isnan(orc.to_float(want, dtype))
-                assert_sum(got[ok], want[ok], dtype, f"op {op} run {rep}")
+                check_sum(got[ok], want[ok], dtype, f"op {op} run {rep}", a, [1], op == MEAN, mask=ok)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -109,10 +126,9 @@ def test_few_long_rows_folded_in_one_launch(dev, ops, orc, dtype, shape):
     dims = None if len(shape) == 1 else [-1]
     for op, fn in ((SUM, ops.sum), (MEAN, ops.mean)):
         want = oracle_reduce(orc, op, dtype, a, dims)
-        count = shape[-1] if op == MEAN else 1
         for rep in range(2):
             got = (fn(d) if dims is None else (ops.sum_dim if op == SUM else ops.mean_dim)(d, dims)).numpy()
-            assert_sum(got, want, dtype, f"op {op} {shape} run {rep}", count)
+            check_sum(got, want, dtype, f"op {op} {shape} run {rep}", a, dims, op == MEAN)
     b = a.copy()
     b.reshape(-1)[shape[-1] // 3] = orc.from_float(np.array([np.nan], np.float32), dtype)[0]
     db = dev.from_numpy(b, dtype=dtype)
@@ -130,22 +146,23 @@ def test_long_reductions(dev, ops, orc, dtype):
     for shape in ((2, 4096), (2, 65536), (16, 8192), (3, 32768), (4096, 2)):
         a = sample(orc, shape, dtype, mean=m)
         d = dev.from_numpy(a, dtype=dtype)
-        assert_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, f"sum {shape}")
-        assert_sum(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype, f"mean {shape}",
-                   int(np.prod(shape)))
-        assert_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype,
-                   f"sum dim 1 {shape}")
-        assert_sum(ops.mean_dim(d, 0).numpy(), oracle_reduce(orc, MEAN, dtype, a, [0]), dtype,
-                   f"mean dim 0 {shape}", shape[0])
+        check_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, f"sum {shape}", a, None)
+        check_sum(ops.mean(d).numpy(), oracle_reduce(orc, MEAN, dtype, a, None), dtype, f"mean {shape}",
+                  a, None, True)
+        check_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype,
+                  f"sum dim 1 {shape}", a, [1])
+        check_sum(ops.mean_dim(d, 0).numpy(), oracle_reduce(orc, MEAN, dtype, a, [0]), dtype,
+                  f"mean dim 0 {shape}", a, [0], True)
         assert_bitexact(ops.amax(d, 0).numpy(), oracle_reduce(orc, AMAX, dtype, a, [0]), "amax 0")
     a = sample(orc, (65537,), dtype, mean=m)
     d = dev.from_numpy(a, dtype=dtype)
-    assert_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, "sum 65537")
+    check_sum(ops.sum(d).numpy(), oracle_reduce(orc, SUM, dtype, a, None), dtype, "sum 65537", a, None)
     assert_bitexact(ops.amin(d).numpy(), oracle_reduce(orc, AMIN, dtype, a, None), "amin all")
     a = sample(orc, (2, 4096, 2), dtype, mean=m)
     d = dev.from_numpy(a, dtype=dtype)
-    assert_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, "sum mid")
-    assert_sum(ops.mean_dim(d, 1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [1]), dtype, "mean mid", 4096)
+    check_sum(ops.sum_dim(d, 1).numpy(), oracle_reduce(orc, SUM, dtype, a, [1]), dtype, "sum mid", a, [1])
+    check_sum(ops.mean_dim(d, 1).numpy(), oracle_reduce(orc, MEAN, dtype, a, [1]), dtype, "mean mid", a, [1],
+              True)
     a = sample(orc, (16, 8192), dtype)
     d = dev.from_numpy(a, dtype=dtype)
     assert_bitexact(ops.amax(d, -1).numpy(), oracle_reduce(orc, AMAX, dtype, a, [-1]), "amax -1")
@@ -212,17 +229,18 @@ def test_reductions_of_permuted_views(dev, ops, orc, dtype):
     d = dev.from_numpy(a, dtype=dtype)
     at = np.ascontiguousarray(a.T)
     for dims in ([0], [1], None):
-        assert_sum(ops.sum_dim(d.t(), dims or []).numpy() if dims else ops.sum(d.t()).numpy(),
-                   oracle_reduce(orc, SUM, dtype, at, dims), dtype, f"sum of .t() over {dims}")
+        check_sum(ops.sum_dim(d.t(), dims or []).numpy() if dims else ops.sum(d.t()).numpy(),
+                  oracle_reduce(orc, SUM, dtype, at, dims), dtype, f"sum of .t() over {dims}", at, dims)
     assert_bitexact(ops.amax(d.t(), [0]).numpy(), oracle_reduce(orc, AMAX, dtype, at, [0]), "amax of .t()")
     b = sample(orc, (6, 40, 24), dtype, 12)
     db = dev.from_numpy(b, dtype=dtype)
     perm = db._view([24, 6, 40], [1, 960, 24])      # b.transpose(2, 0, 1), no copy
     bp = np.ascontiguousarray(np.transpose(b, (2, 0, 1)))
-    assert_sum(ops.sum_dim(perm, [1]).numpy(), oracle_reduce(orc, SUM, dtype, bp, [1]), dtype,
-               "sum over dim 1 of a permutation (kept dims reordered)")
+    check_sum(ops.sum_dim(perm, [1]).numpy(), oracle_reduce(orc, SUM, dtype, bp, [1]), dtype,
+              "sum over dim 1 of a permutation (kept dims reordered)", bp, [1])
     got = ops.sum_dim(perm, [0, 2], keepdim=True).numpy()
-    assert_sum(got, oracle_reduce(orc, SUM, dtype, bp, [0, 2], True), dtype, "sum (0, 2) of a permutation")
+    check_sum(got, oracle_reduce(orc, SUM, dtype, bp, [0, 2], True), dtype, "sum (0, 2) of a permutation",
+              bp, [0, 2], keepdim=True)
     assert_bitexact(ops.amin(perm, [2]).numpy(), oracle_reduce(orc, AMIN, dtype, bp, [2]), "amin of a permutation")
 
 
@@ -248,17 +266,53 @@ def test_softmax_and_log_softmax(dev, ops, orc, dtype, dim, shape):
     for log, fn in ((False, ops.softmax), (True, ops.log_softmax)):
         y = fn(d, dim)
         want = orc.softmax(log, dtype, a, outer, size, inner)
-        # log_softmax of -inf is -inf: infinities must match in place and
-        # sign, the finite entries norm-wise
-        got_f, want_f = as_float(y.numpy(), dtype), as_float(want, dtype)
-        inf = np.isinf(want_f)
-        assert np.array_equal(np.isinf(got_f), inf) and np.array_equal(got_f[inf], want_f[inf]), "infinities"
-        assert_normwise(y.numpy()[~inf], want[~inf], dtype, 1, f"softmax log={log}")
+        # log_softmax of -inf is -inf: the checker matches infinities in
+        # place and sign, the finite entries per element
+        yh = y.numpy()
+        assert_softmax(yh, want, dtype, log, f"softmax log={log}")
         g = sample(orc, a.shape, dtype, 9)
         back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
         got = back(dev.from_numpy(g, dtype=dtype), y, dim, dtype).numpy()
-        assert_normwise(got, orc.softmax_backward(log, dtype, y.numpy(), g, outer, size, inner),
-                        dtype, 1, f"softmax backward log={log}")
+        assert_softmax_backward(got, orc.softmax_backward(log, dtype, yh, g, outer, size, inner), dtype, log,
+                                yh, g, outer, size, inner, f"softmax backward log={log}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape,dim", [((3, 130), 0), ((2, 5, 70), 1), ((4, 300, 130), 0)],
+                         ids=["3x130-dim0", "2x5x70-dim1", "4x300x130-dim0"])
+def test_softmax_nan_over_a_leading_axis(dev, ops, orc, dtype, shape, dim):
+    """A NaN makes its whole softmax line NaN, also over a leading axis
+    where a wave's batch of rows can hold nothing but that NaN, masked rows
+    and -inf: forward and backward, against the oracle (NaN in the same
+    places, the rest per element)."""
+    a = sample(orc, shape, dtype, 21)
+    nan = orc.from_float(np.array([np.nan], np.float32), dtype)[0]
+    ninf = orc.from_float(np.array([-np.inf], np.float32), dtype)[0]
+    idx = [0] * len(shape)
+    a[tuple(idx)] = nan                        # row 0 of column 0
+    idx[-1] = 7
+    a[tuple(idx)] = nan                        # a second column: NaN, the rest -inf
+    sl = [slice(None)] * len(shape)
+    sl[-1] = 7
+    col = a[tuple(sl)]
+    sel = [slice(None)] * col.ndim
+    sel[dim] = slice(1, None)
+    col[tuple(sel)] = ninf
+    a[tuple(sl)] = col
+    d = dev.from_numpy(a, dtype=dtype)
+    k = dim % len(shape)
+    outer, size, inner = int(np.prod(shape[:k])), shape[k], int(np.prod(shape[k + 1:]))
+    g = sample(orc, shape, dtype, 22)
+    for log in (False, True):
+        y = (ops.log_softmax if log else ops.softmax)(d, dim)
+        yh = y.numpy()
+        want = orc.softmax(log, dtype, a, outer, size, inner)
+        assert np.isnan(as_float(want, dtype)).sum() >= 2 * size
+        assert_softmax(yh, want, dtype, log, f"forward log={log}")
+        back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
+        got = back(dev.from_numpy(g, dtype=dtype), y, dim, dtype).numpy()
+        assert_softmax_backward(got, orc.softmax_backward(log, dtype, yh, g, outer, size, inner), dtype, log,
+                                yh, g, outer, size, inner, f"backward log={log}")
 
 
 @pytest.mark.parametrize("D", [1, 7, 64, 256, 1000, 1024, 4096, 4100, 16384, 32000, 65536, 70000])
@@ -270,13 +324,13 @@ def test_softmax_row_lengths(dev, ops, orc, D):
         d = dev.from_numpy(a, dtype=dtype)
         for log in (False, True):
             y = (ops.log_softmax if log else ops.softmax)(d, -1)
-            assert_normwise(y.numpy(), orc.softmax(log, dtype, a, rows, D, 1), dtype, 1,
-                            f"D={D} log={log}")
+            yh = y.numpy()
+            assert_softmax(yh, orc.softmax(log, dtype, a, rows, D, 1), dtype, log, f"D={D} log={log}")
             g = sample(orc, (rows, D), dtype, 2)
             back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
             got = back(dev.from_numpy(g, dtype=dtype), y, -1, dtype).numpy()
-            assert_normwise(got, orc.softmax_backward(log, dtype, y.numpy(), g, rows, D, 1),
-                            dtype, 1, f"backward D={D} log={log}")
+            assert_softmax_backward(got, orc.softmax_backward(log, dtype, yh, g, rows, D, 1), dtype, log,
+                                    yh, g, rows, D, 1, f"backward D={D} log={log}")
 
 
 @pytest.mark.parametrize("rows,D,dtype", [(600, 8200, F32), (1000, 20000, F32), (257, 32000, F32),
@@ -288,8 +342,8 @@ def test_softmax_rows_walked_by_one_block_per_cu(dev, ops, orc, rows, D, dtype):
     d = dev.from_numpy(a, dtype=dtype)
     for log in (False, True):
         y = (ops.log_softmax if log else ops.softmax)(d, -1)
-        assert_normwise(y.numpy(), orc.softmax(log, dtype, a, rows, D, 1), dtype, 1,
-                        f"rows={rows} D={D} log={log}")
+        assert_softmax(y.numpy(), orc.softmax(log, dtype, a, rows, D, 1), dtype, log,
+                       f"rows={rows} D={D} log={log}")
 
 
 def test_softmax_declines(dev, ops, orc):
@@ -313,10 +367,10 @@ def test_config3_full_size(dev, ops, orc, dtype, shape, std):
     d = dev.from_numpy(a, dtype=dtype)
     R, C = shape
     for dim, (outer, r, inner) in ((-1, (R, C, 1)), (0, (1, R, C))):
-        assert_sum(ops.sum_dim(d, dim).numpy(), orc.reduce(SUM, dtype, a, outer, r, inner),
-                   dtype, f"sum dim {dim}")
-        assert_sum(ops.mean_dim(d, dim).numpy(), orc.reduce(MEAN, dtype, a, outer, r, inner),
-                   dtype, f"mean dim {dim}", r)
+        check_sum(ops.sum_dim(d, dim).numpy(), orc.reduce(SUM, dtype, a, outer, r, inner),
+                  dtype, f"sum dim {dim}", a, [dim])
+        check_sum(ops.mean_dim(d, dim).numpy(), orc.reduce(MEAN, dtype, a, outer, r, inner),
+                  dtype, f"mean dim {dim}", a, [dim], True)
         assert_bitexact(ops.amax(d, dim).numpy(), orc.reduce(AMAX, dtype, a, outer, r, inner),
                         f"amax dim {dim}")
         assert_bitexact(ops.amin(d, dim).numpy(), orc.reduce(AMIN, dtype, a, outer, r, inner),
@@ -326,8 +380,7 @@ def test_config3_full_size(dev, ops, orc, dtype, shape, std):
     for log in (False, True):
         y = (ops.log_softmax if log else ops.softmax)(d, -1)
         yh = y.numpy()
-        assert_normwise(yh, orc.softmax(log, dtype, a, R, C, 1), dtype, 1, f"softmax log={log}")
+        assert_softmax(yh, orc.softmax(log, dtype, a, R, C, 1), dtype, log, f"softmax log={log}")
         back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
-        assert_normwise(back(dg, y, -1, dtype).numpy(),
-                        orc.softmax_backward(log, dtype, yh, g, R, C, 1), dtype, 1,
-                        f"softmax backward log={log}")
+        assert_softmax_backward(back(dg, y, -1, dtype).numpy(), orc.softmax_backward(log, dtype, yh, g, R, C, 1),
+                                dtype, log, yh, g, R, C, 1, f"softmax backward log={log}")

@@ -63,4 +63,6 @@ def test_noalloc_matches_allocating_entry(amd, dev, ops, orc, pair):
             if op in (AMAX, AMIN):
                 assert_bitexact(got.numpy(), want, what)
             else:
-                assert_sum(got.numpy(), want, dtype, what, r if op == MEAN else 1)
+                mag = np.abs(orc.to_float(x, dtype).astype(np.float64)).sum(axis=1).reshape(-1)
+                assert_sum(got.numpy(), want, dtype, what, r if op == MEAN else 1,
+                           mag / r if op == MEAN else mag, r)
