@@ -52,6 +52,9 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 # for a copy kernel of known size; recorded in
 # profiles/config2_binary2d_hbm_traffic.md.
 DOMINANT_TRAFFIC_BYTES = 536829485
+# The same for the cold rotation (``bench.py --profile traffic_cold``),
+# recorded in the same file.
+COLD_TRAFFIC_BYTES = 536765611
 MFMA_PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 METRIC = "GEMM TFLOP/s + %MFMA peak; reduce/softmax/eltwise GB/s + %HBM peak"
 N = 8192
@@ -156,7 +159,48 @@ def dominant_kernel(lib, ev, t, reps=50):
     return {"kernel": "binary2d_kernel<float, full, row-broadcast> (add)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "cache": "warm: one input and one output reused on every launch (the Infinity Cache "
+                     "keeps part of the 256 MiB input)",
             "traffic": DOMINANT_TRAFFIC_BYTES,
+            "avg_us": round(ms * 1e3, 2), "algorithmic_bytes_per_launch": algo}
+
+
+COLD_PAIRS = 4  # input/output pairs the cold measurement rotates over
+
+
+def dominant_kernel_cold(lib, ops, ev, t, rounds=12):
+    """The dominant kernel with its working set beyond the 256 MB Infinity
+    Cache: COLD_PAIRS distinct [8192, 8192] float32 inputs and outputs (2 GiB
+    in all), launched round-robin, so every launch reads an input and
+    writes an output last touched COLD_PAIRS - 1 launches (1.5 GiB of other
+    traffic) earlier.  Average launch duration over ``rounds`` rotations,
+    from HIP events on the library's stream."""
+    import ctypes as C
+    a, row = t["a"], t["row"]
+    inputs = [a] + [ops.add_scalar(a, float(k)) for k in range(1, COLD_PAIRS)]
+    outputs = [ops.empty((N, N), F32) for _ in range(COLD_PAIRS)]
+    sizes = (C.c_int64 * 2)(N, N)
+    sa = (C.c_int64 * 2)(N, 1)
+    sb = (C.c_int64 * 2)(0, 1)
+
+    def rotation():
+        for x, y in zip(inputs, outputs):
+            st = lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, x.data_ptr, sa, row.data_ptr, sb, y.data_ptr, sa,
+                                          1.0)
+            assert st == 0
+
+    for _ in range(3):
+        rotation()
+    ms = ev.time_ms(rotation, rounds) / COLD_PAIRS
+    algo = 2 * N * N * 4
+    achieved = algo / (ms * 1e-3) / 1e9
+    del inputs, outputs
+    return {"kernel": "binary2d_kernel<float, full, row-broadcast> (add)",
+            "cache": f"cold: {COLD_PAIRS} inputs and {COLD_PAIRS} outputs of 256 MiB rotated "
+                     f"({COLD_PAIRS * 512} MiB working set, 256 MB Infinity Cache)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": COLD_TRAFFIC_BYTES,
             "avg_us": round(ms * 1e3, 2), "algorithmic_bytes_per_launch": algo}
 
 
@@ -822,6 +866,9 @@ def profile_launches(what: str, lib, ops, dev) -> None:
     traffic: ten launches of a copy-like kernel (affine y = 1 x + 0 on
              [8192, 8192] float32, 2 x 268,435,456 B) to calibrate the
              FETCH_SIZE / WRITE_SIZE counters, then ten of the dominant kernel;
+    traffic_cold: the same calibration, then sixteen launches of the
+             dominant kernel rotating over four inputs and four outputs
+             (the cold measurement's sequence);
     gemm:    ten bf16 4096^3 products in each operand layout (A, B
              row-major; B transposed; A transposed; both transposed);
     gemm32:  the same in float32, five products a layout;
@@ -847,7 +894,21 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              [4096, 50257]; then binary ops with transposed inputs, fp32 and
              bf16 4096^2, ten x.t() + y and ten x.t() * y.t() each."""
     import ctypes as C
-    if what == "traffic":
+    if what == "traffic_cold":
+        a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
+        row = dev.from_numpy(np.full((N,), 0.5, np.float32))
+        out = ops.empty((N, N), F32)
+        for _ in range(10):
+            assert lib.tp_amd_launch_affine(0, F32, N * N, a.data_ptr, 1.0, 0.0, out.data_ptr) == 0
+        inputs = [a] + [ops.add_scalar(a, float(k)) for k in range(1, COLD_PAIRS)]
+        outputs = [out] + [ops.empty((N, N), F32) for _ in range(1, COLD_PAIRS)]
+        sizes = (C.c_int64 * 2)(N, N)
+        sa, sb = (C.c_int64 * 2)(N, 1), (C.c_int64 * 2)(0, 1)
+        for _ in range(4):
+            for x, y in zip(inputs, outputs):
+                assert lib.tp_amd_launch_binary(0, 0, F32, 2, sizes, x.data_ptr, sa, row.data_ptr, sb,
+                                                y.data_ptr, sa, 1.0) == 0
+    elif what == "traffic":
         a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
         row = dev.from_numpy(np.full((N,), 0.5, np.float32))
         out = ops.empty((N, N), F32)
@@ -994,7 +1055,7 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "gemm", "gemm32", "linear", "bmm", "reduce", "reduce_all",
+    p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "bmm", "reduce", "reduce_all",
                                          "softmax", "nn", "mlp", "odd"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
@@ -1039,8 +1100,9 @@ def main() -> int:
     secs = time.perf_counter() - t0
     value = step_bytes * args.steps / secs / 1e9
 
-    log("bench: dominant kernel")
-    roofline = dominant_kernel(lib, ev, tensors[F32])
+    log("bench: dominant kernel, warm and cold")
+    roofline_warm = dominant_kernel(lib, ev, tensors[F32])
+    roofline = dominant_kernel_cold(lib, ops, ev, tensors[F32])
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
@@ -1052,6 +1114,7 @@ def main() -> int:
                    "shape": [N, N], "storage_dtypes": ["fp32", "bf16"],
                    "bytes_per_step": step_bytes, "parallelism": "single GPU"},
         "roofline": roofline,
+        "roofline_warm": roofline_warm,
     }
     if not args.no_suite:
         def section(name, fn):
@@ -1064,7 +1127,11 @@ def main() -> int:
                 log(f"bench: suite {name} failed: {exc!r}")
                 return {"error": repr(exc)}
 
-        suite = {"config2": section("config 2", lambda: suite_config2(ops, ev, tensors))}
+        suite = {"timing": "config2..nn: average of back-to-back calls between two HIP events on the "
+                           "library's stream (10 calls; 5 for GEMM, 3 for the MLP step) after 2 untimed; "
+                           "readme_rows: median of 50 single-call HIP-event pairs after 5 untimed, the "
+                           "reference README's method (host copies: wall clock)"}
+        suite["config2"] = section("config 2", lambda: suite_config2(ops, ev, tensors))
         del tensors
         suite["config3"] = section("config 3", lambda: suite_config3(ops, dev, ev))
         suite["config4_5a"] = section("configs 4 and 5a", lambda: suite_gemm(ops, dev, ev))
