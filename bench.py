@@ -15,7 +15,10 @@ timed steps.
 Also reported on the same line:
 * ``roofline``: the dominant kernel (the broadcasting binary kernel, float32
   add against a row-broadcast operand), its average launch duration from
-  HIP events recorded on the library's own stream, against 8 TB/s;
+  HIP events recorded on the library's own stream, against 8 TB/s, measured
+  cold: four inputs and four outputs rotated, 2 GiB, beyond the 256 MB
+  Infinity Cache; ``roofline_warm`` is the same kernel on one input and
+  output reused every launch;
 * ``suite``: per-kernel throughput of configs 2-5 and of the neural-network
   layers (GB/s or TFLOP/s and the fraction of the matching MI355X peak), each
   from HIP events, and the reference README's benchmark rows beside the
