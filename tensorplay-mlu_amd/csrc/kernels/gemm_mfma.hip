@@ -1074,8 +1074,14 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
 // odd K or leading dimension: a vocabulary of 50257, a Linear(1023, ...), a
 // column slice at an odd offset) copy that operand into a dense K-major
 // workspace [batch][M or N][K'], K' = K rounded up to the packet, with the
-// columns K..K' zeroed; an odd K repacks both operands, so the padded terms
-// are 0 x 0.  The copies cost a pass over the operands; the general kernel
+// columns K..K' zeroed.  An odd K alone only forces the K-major operands
+// into such copies (their 16-byte packets run along K and would cross the
+// end of a row); an operand stored with M or N contiguous stays where it
+// is, since the bounds-checked tile loaders give zeros for its rows k >= K,
+// and the product keeps K.  Before, an odd K repacked both operands: the
+// dX = dY W of an LM head with a 50257 vocabulary (bf16 1 x 50257 x 4096)
+// transposed the whole 400 MB weight on every call.  The copies cost a pass
+// over the operands; the general kernel
 // they replace runs ~16x slower than the matrix cores (2047^3 in bfloat16:
 // 692 us there, 63 us repacked).  Products under kRepackMinMacs
 // multiply-adds (about 160^3) keep the general kernel, which needs no
@@ -1145,8 +1151,11 @@ void launch_repacked(const GemmArgs& p, hipStream_t stream) {
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     const int64_t kp = (p.k + V - 1) / V * V;
-    const bool fix_a = kp != p.k || !operand_ok<T>(p.a, p.lda, p.stride_a, !p.trans_a, p.m, p.k);
-    const bool fix_b = kp != p.k || !operand_ok<T>(p.b, p.ldb, p.stride_b, p.trans_b, p.n, p.k);
+    const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
+    // An in-place MN-major operand only needs its own packets aligned; for
+    // the check K is taken as padded (its K extent is not read in packets).
+    const bool fix_a = (a_kmajor && kp != p.k) || !operand_ok<T>(p.a, p.lda, p.stride_a, a_kmajor, p.m, kp);
+    const bool fix_b = (b_kmajor && kp != p.k) || !operand_ok<T>(p.b, p.ldb, p.stride_b, b_kmajor, p.n, kp);
     // A batch-broadcast operand (stride 0) is copied once and stays broadcast.
     const int64_t bs_a = p.stride_a == 0 ? 1 : p.batch, bs_b = p.stride_b == 0 ? 1 : p.batch;
     const size_t bytes_a = fix_a ? static_cast<size_t>(bs_a * p.m * kp) * E : 0;
@@ -1154,7 +1163,10 @@ void launch_repacked(const GemmArgs& p, hipStream_t stream) {
     const size_t bytes_b = fix_b ? static_cast<size_t>(bs_b * p.n * kp) * E : 0;
     Workspace ws(off_b + bytes_b, device);
     GemmArgs q = p;
-    q.k = kp;
+    // Both operands copied: K' with zero terms on both sides (the big
+    // kernels' whole K tiles apply).  Otherwise the in-place operand bounds
+    // the product at K, and the copies' zero columns are never summed in.
+    q.k = fix_a && fix_b ? kp : p.k;
     if (fix_a) {
         repack_kmajor<typename Elem<T>::storage>(device, p.a, p.lda, p.stride_a, !p.trans_a, bs_a, p.m, p.k, kp,
                                                  ws.get(), stream);

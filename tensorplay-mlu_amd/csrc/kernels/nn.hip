@@ -994,7 +994,7 @@ __global__ __launch_bounds__(kBlock) void embedding_fill_kernel(const void* idx,
 // Row `row` of the gradient = the sum of dy's rows entries[0 .. c) in that
 // order (float32, from 0), times 1 / c with scale_grad_by_freq; the block's
 // threads split the columns.
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NT = true>
 __device__ __forceinline__ void sum_row(const S_<T>* dy, const int* entries, int c, int64_t D,
                                         int scale_grad_by_freq, S_<T>* row) {
     constexpr int N = VEC ? Packet<T>::N : 1;
@@ -1018,20 +1018,22 @@ __device__ __forceinline__ void sum_row(const S_<T>* dy, const int* entries, int
 #pragma unroll
         for (int j = 0; j < N; ++j) acc[j] *= scale;
         if constexpr (VEC) {
-            store_raw_nt(row + q * N, pack<T>(acc));
+            if constexpr (NT) store_raw_nt(row + q * N, pack<T>(acc));
+            else *reinterpret_cast<uint4*>(row + q * N) = pack<T>(acc);
         } else {
             row[q] = Elem<T>::store(acc[0]);
         }
     }
 }
 
-// Row `row` of zeros.
-template <typename T, bool VEC>
+// Row `row` of zeros (NT: non-temporal stores).
+template <typename T, bool VEC, bool NT = true>
 __device__ __forceinline__ void zero_row(int64_t D, S_<T>* row) {
     constexpr int N = VEC ? Packet<T>::N : 1;
     for (int64_t q = threadIdx.x; q < D / N; q += kBlock) {
         if constexpr (VEC) {
-            store_raw_nt(row + q * N, make_uint4(0u, 0u, 0u, 0u));
+            if constexpr (NT) store_raw_nt(row + q * N, make_uint4(0u, 0u, 0u, 0u));
+            else *reinterpret_cast<uint4*>(row + q * N) = make_uint4(0u, 0u, 0u, 0u);
         } else {
             row[q] = Elem<T>::store(0.0f);
         }
@@ -1242,7 +1244,14 @@ __global__ __launch_bounds__(kRangeThreads) void embedding_plan_range_kernel(con
 
 // Row r of the gradient (one block) from a plan whose rows list their
 // samples in increasing order: list[starts[r] .. starts[r] + counts[r]).
-template <typename T, bool VEC>
+// NT selects non-temporal stores: the host takes them for a table larger
+// than the 256 MB Infinity Cache, and the default policy for one that fits
+// (measured on [32000, 4096] with 8192 random indices: bf16, 262 MB, 58.6 us
+// against 69.8 us non-temporal; float32, 524 MB, 131.8 us against 138.1 us
+// with the default policy).
+constexpr int64_t kGatherCachedBytes = int64_t{256} << 20;
+
+template <typename T, bool VEC, bool NT>
 __global__ __launch_bounds__(kBlock) void embedding_gather_ordered_kernel(const S_<T>* dy, const int* starts,
                                                                           const int* counts, const int* list,
                                                                           int n_list, int64_t D,
@@ -1253,9 +1262,9 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_ordered_kernel(const 
     const int c = max(0, min(counts[r], n_list - off));
     S_<T>* row = out + r * D;
     if (c == 0) {
-        zero_row<T, VEC>(D, row);
+        zero_row<T, VEC, NT>(D, row);
     } else {
-        sum_row<T, VEC>(dy, list + off, c, D, scale_grad_by_freq, row);
+        sum_row<T, VEC, NT>(dy, list + off, c, D, scale_grad_by_freq, row);
     }
     // Last, after every load: a store ahead of them would make the compiler
     // read starts and counts through vector memory instead of scalar loads
@@ -1594,14 +1603,19 @@ int tp_amd_launch_embedding_backward(int device, int dtype, int64_t n, int64_t d
             });
             TP_AMD_DISPATCH_NN(dtype, T, {
                 const bool vec = dim % Packet<T>::N == 0 && aligned16(grad) && aligned16(out);
+                const bool nt = num_weights * dim * static_cast<int64_t>(sizeof(S_<T>)) > kGatherCachedBytes;
+                auto gather = [&](auto vec_tag, auto nt_tag) {
+                    embedding_gather_ordered_kernel<T, decltype(vec_tag)::value, decltype(nt_tag)::value>
+                        <<<num_weights, kBlock, 0, st>>>(static_cast<const S_<T>*>(grad), starts, counts, list,
+                                                        static_cast<int>(regions * n), dim, scale_grad_by_freq,
+                                                        static_cast<S_<T>*>(out));
+                };
+                using Yes = std::true_type;
+                using No = std::false_type;
                 if (vec) {
-                    embedding_gather_ordered_kernel<T, true><<<num_weights, kBlock, 0, st>>>(
-                        static_cast<const S_<T>*>(grad), starts, counts, list, static_cast<int>(regions * n),
-                        dim, scale_grad_by_freq, static_cast<S_<T>*>(out));
+                    nt ? gather(Yes{}, Yes{}) : gather(Yes{}, No{});
                 } else {
-                    embedding_gather_ordered_kernel<T, false><<<num_weights, kBlock, 0, st>>>(
-                        static_cast<const S_<T>*>(grad), starts, counts, list, static_cast<int>(regions * n),
-                        dim, scale_grad_by_freq, static_cast<S_<T>*>(out));
+                    nt ? gather(No{}, Yes{}) : gather(No{}, No{});
                 }
             });
             TP_AMD_HIP_CHECK(hipGetLastError());

@@ -159,7 +159,10 @@ __device__ __forceinline__ uint4 splat(uint32_t w) { return make_uint4(w, w, w, 
 // batch's out-of-range slots padded with a value that leaves the result
 // unchanged, so every batch's loads are in flight together.  Float combine
 // in element order.
-template <typename Tin, int OP, int THREADS, int U = 4>
+// NT: non-temporal loads (the default for rows streamed once); false keeps
+// the default policy, under which a tensor the previous kernel left in the
+// 256 MB Infinity Cache is read from there.
+template <typename Tin, int OP, int THREADS, int U = 4, bool NT = true>
 __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p, int64_t pb,
                                            int64_t pe, int tid) {
     constexpr int N = Packet<Tin>::N;
@@ -174,7 +177,8 @@ __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p,
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t q = q0 + static_cast<int64_t>(u) * THREADS;
-            raw[u] = q < pe ? load_raw_nt(p + q * N) : splat(kPad);
+            raw[u] = q < pe ? (NT ? load_raw_nt(p + q * N) : *reinterpret_cast<const uint4*>(p + q * N))
+                            : splat(kPad);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -190,7 +194,7 @@ __device__ __forceinline__ float row_exact(const typename Elem<Tin>::storage* p,
 // The same share for amax / amin on integer keys (NaN when a NaN wins or the
 // share is empty).  The padding is the NaN pattern whose key loses to every
 // value.
-template <typename Tin, int OP, int THREADS, int U = 4>
+template <typename Tin, int OP, int THREADS, int U = 4, bool NT = true>
 __device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, int64_t pb,
                                           int64_t pe, int tid) {
     constexpr int N = Packet<Tin>::N;
@@ -204,7 +208,8 @@ __device__ __forceinline__ float row_keys(const typename Elem<Tin>::storage* p, 
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t q = q0 + static_cast<int64_t>(u) * THREADS;
-            raw[u] = q < pe ? load_raw_nt(p + q * N) : splat(kPad);
+            raw[u] = q < pe ? (NT ? load_raw_nt(p + q * N) : *reinterpret_cast<const uint4*>(p + q * N))
+                            : splat(kPad);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -339,12 +344,18 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
     const int tid = threadIdx.x;
     float acc = Combine<OP>::identity();
     if constexpr (VEC) {
+        // 16-bit tensors load with the default policy, float32 ones
+        // non-temporally.  Measured on whole 4096^2 tensors called back to
+        // back: bf16 sum 5.86 us against 8.32 us non-temporal (the 32 MiB
+        // are served from the Infinity Cache), float32 11.0 us against
+        // 12.6 us with the default policy.
+        constexpr bool kNt = sizeof(typename Elem<Tin>::storage) == 4;
         const int64_t pb = begin / N, pe = end / N;
         if constexpr (kMinMax<OP>) {
-            acc = row_keys<Tin, OP, kBlock, 8>(p, pb, pe, tid);
-            if (acc != acc) acc = row_exact<Tin, OP, kBlock, 8>(p, pb, pe, tid);
+            acc = row_keys<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
+            if (acc != acc) acc = row_exact<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
         } else {
-            acc = row_exact<Tin, OP, kBlock, 8>(p, pb, pe, tid);
+            acc = row_exact<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
         }
     } else {
         for (int64_t j = begin + tid; j < end; j += kBlock) {

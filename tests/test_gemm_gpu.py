@@ -355,6 +355,56 @@ def test_gemm_abi_repacked_operands(amd, dev, orc, dtype, ta, tb, bt, m, n, k, p
     check(orc, got, want, dtype, f"gemm abi {bt}x{m}x{n}x{k} ta={ta} tb={tb}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True)], ids=["NN", "TT"])
+def test_gemm_abi_odd_k_in_place_mn_major(amd, dev, orc, dtype, ta, tb):
+    """An odd K with one operand stored M/N-contiguous and aligned: only the
+    K-major operand is copied (zero-padded to whole packets), the other is
+    read in place up to row K -- its storage has NaN rows right after row
+    K, which must never reach the product."""
+    lib = amd.load()
+    bt, m, n, k, alpha, beta = 2, 264, 256, 509, 0.5, 2.0  # M, N and their lds whole packets
+    g = np.random.default_rng(5)
+    # the K-major operand: ordinary storage, ld = K
+    km = g.standard_normal((bt, n, k) if tb else (bt, m, k)).astype(np.float32) * np.float32(0.25)
+    km = orc.from_float(km, dtype)
+    # the MN-major operand: [K + 5, MN + 8] per batch, NaN past row K and column MN
+    mn_len = m if ta else n
+    store = np.full((bt, k + 5, mn_len + 8), np.nan, np.float32)
+    store[:, :k, :mn_len] = g.standard_normal((bt, k, mn_len)).astype(np.float32) * np.float32(0.25)
+    mnm = orc.from_float(store, dtype)
+    cin = sample(orc, (bt, m, n), dtype, 3)
+    d_km, d_mn, dc = (dev.from_numpy(x, dtype=dtype) for x in (km, mnm, cin))
+    out = dev.empty((bt, m, n), dtype=dtype)
+    ld_mn, sb_mn = mn_len + 8, (k + 5) * (mn_len + 8)
+    if ta:   # A stored [K, M] (M contiguous) in place, B stored [N, K] (K-major)
+        args = (d_mn.data_ptr, ld_mn, sb_mn, 1, d_km.data_ptr, k, n * k, 1)
+    else:    # A stored [M, K] (K-major), B stored [K, N] (N contiguous) in place
+        args = (d_km.data_ptr, k, m * k, 0, d_mn.data_ptr, ld_mn, sb_mn, 0)
+    st = lib.tp_amd_launch_gemm(0, dtype, bt, m, n, k, alpha, *args, beta, dc.data_ptr, n, 1, m * n,
+                                out.data_ptr, n, m * n)
+    assert st == 0, lib.tp_mlu_last_error()
+    K = orc.to_float(km, dtype)
+    Mv = orc.to_float(mnm, dtype)[:, :k, :mn_len]
+    A = np.swapaxes(Mv, 1, 2) if ta else K
+    B = np.swapaxes(K, 1, 2) if tb else Mv
+    want = alpha * np.matmul(A, B) + beta * orc.to_float(cin, dtype)
+    got = out.numpy()
+    assert not np.isnan(orc.to_float(got, dtype)).any(), "rows past K leaked into the product"
+    check(orc, got, want, dtype, f"odd K in place ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_mm_skinny_odd_k(dev, ops, orc, dtype):
+    """dX = dY W for a one-row dY and a vocabulary-sized odd K (W stored
+    [K, N], N contiguous): read in place, checked against the float64
+    product."""
+    dy = sample(orc, (1, 3001), dtype, 21)
+    w = sample(orc, (3001, 256), dtype, 22, 3001 ** -0.5)
+    got = ops.mm(dev.from_numpy(dy, dtype=dtype), dev.from_numpy(w, dtype=dtype)).numpy()
+    check(orc, got, exact(orc, dy, w, dtype), dtype, "skinny odd K")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
 def test_mm_2047_cube(dev, ops, orc, dtype):
     """mm 2047^3 (odd everything) through ops.mm, checked on sampled
