@@ -121,6 +121,16 @@ int tp_amd_launch_reduce_noalloc(int device, int op, int dtype, int64_t outer, i
 /* Size in bytes of the static partials array of tp_amd_launch_reduce_noalloc. */
 size_t tp_amd_reduce_noalloc_scratch_bytes(void);
 
+/* No counterpart in the reference: a planning query for callers of
+ * tp_amd_launch_reduce_noalloc.  The bytes of float32 partials that a
+ * reduction of dense [outer, r, inner] ``dtype`` with a 16-byte aligned input
+ * uses on a GPU with ``compute_units`` CUs (0 when it runs without partials;
+ * -1 for an unknown dtype or a negative extent).  The allocation-free entry
+ * refuses the shapes whose figure exceeds tp_amd_reduce_noalloc_scratch_bytes();
+ * pure host arithmetic, no GPU needed. */
+int64_t tp_amd_reduce_partial_bytes(int compute_units, int dtype, int64_t outer, int64_t r,
+                                    int64_t inner);
+
 /* Replaces cnnlSoftmaxForward (ReduceKernels.cpp:171-183): x, y dense
  * [outer, dim, inner] of ``dtype``; softmax (log_softmax when ``log``) along
  * the middle axis, float32 arithmetic. */

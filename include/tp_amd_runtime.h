@@ -78,6 +78,10 @@ int tp_amd_set_device(int index);
 int tp_amd_synchronize(int index);
 /* memory_info (MLUHooks.cpp:46-51): free and total bytes from the driver. */
 int tp_amd_mem_get_info(int index, size_t* free_bytes, size_t* total_bytes);
+/* The device's compute units (the figure the kernels size their grids by;
+ * stands where the reference's capability() query does,
+ * MLURuntime.cpp:54-67); index < 0 means the current device. */
+int tp_amd_compute_units(int index, int* units);
 /* copy_bytes (MLUHooks.cpp:23-44): device -1 is host memory.  Host copies
  * return once the bytes have landed (MLURuntime.cpp:112-129); a copy on one
  * device is ordered on its stream; between two devices it bounces through

@@ -102,6 +102,7 @@ PROTOTYPES = {
     "tp_amd_set_device": (i32, [i32]),
     "tp_amd_synchronize": (i32, [i32]),
     "tp_amd_mem_get_info": (i32, [i32, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "tp_amd_compute_units": (i32, [i32, C.POINTER(C.c_int)]),
     "tp_amd_copy_bytes": (i32, [VP, i32, VP, i32, C.c_size_t]),
     "tp_amd_stream": (i32, [i32, C.POINTER(VP)]),
     "tp_amd_malloc": (i32, [C.c_size_t, i32, C.POINTER(VP), C.POINTER(VP)]),
@@ -127,6 +128,7 @@ PROTOTYPES = {
     "tp_amd_launch_reduce": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
     "tp_amd_launch_reduce_noalloc": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
     "tp_amd_reduce_noalloc_scratch_bytes": (C.c_size_t, []),
+    "tp_amd_reduce_partial_bytes": (i64, [i32, i32, i64, i64, i64]),
     "tp_amd_launch_softmax": (i32, [i32, i32, i32, i64, i64, i64, VP, VP]),
     "tp_amd_launch_softmax_backward": (i32, [i32, i32, i32, i64, i64, i64, VP, VP, VP]),
     "tp_amd_launch_gemm": (i32, [i32, i32, i64, i64, i64, i64, f32, VP, i64, i64, i32, VP, i64,

@@ -641,6 +641,67 @@ private:
     float* ptr_ = nullptr;
 };
 
+// How a reduction of [outer, r, inner] is split, decided on the host from
+// the shape, the packet width and the CU count alone, so that the launch
+// and the partials-size query (tp_amd_reduce_partial_bytes) agree.
+//   inner == 1 (rows): rows short or many enough run one segment per row;
+//     otherwise each row is cut into nseg segments of `chunk` elements
+//     (about two blocks per CU, at least 4096 elements each) whose float32
+//     partials the last block of the row folds.
+//   inner > 1 (columns): bx column ranges of cols_per_block columns times z
+//     outer indices; with fewer of those than CUs the rows are cut into
+//     nchunk chunks whose partials the last block of a column range folds.
+struct SplitPlan {
+    int64_t nseg = 1, chunk = 0, ngroups = 0;  // rows
+    int64_t bx = 0, z = 0, nchunk = 1;         // columns (chunk: rows a chunk)
+    int64_t partial_floats = 0;
+};
+
+SplitPlan plan_split(int64_t outer, int64_t r, int64_t inner, int64_t cus, int64_t packet, bool vec,
+                     int64_t cols_per_block) {
+    SplitPlan sp;
+    if (inner == 1) {
+        // Measured on a whole 4096^2 float32 tensor: 11.7 us with two blocks
+        // per CU, against 11.9 (four), 13.0 (eight) and 12.8 (one).
+        if (outer < cus * 16 && r >= 8192) {
+            int64_t nseg = (cus * 2 + outer - 1) / outer;
+            const int64_t max_seg = r / 4096;  // >= 2 here
+            if (nseg > max_seg) nseg = max_seg;
+            int64_t chunk = (r + nseg - 1) / nseg;
+            if (vec) chunk = (chunk + packet - 1) / packet * packet;
+            nseg = (r + chunk - 1) / chunk;
+            if (nseg > 1) {
+                sp.nseg = nseg;
+                sp.chunk = chunk;
+                sp.ngroups = (nseg + kFoldGroup - 1) / kFoldGroup;
+                sp.partial_floats = outer * nseg;
+            }
+        }
+        return sp;
+    }
+    sp.bx = (inner + cols_per_block - 1) / cols_per_block;
+    sp.z = outer < 65535 ? outer : 65535;
+    const int64_t base_blocks = sp.bx * sp.z;
+    // About one block per CU, each with eight 16-byte loads per thread in
+    // flight: nchunk = round(CUs / column ranges).  Measured on config 3's
+    // dim-0 reductions against the earlier two blocks per CU: X2 [4096,
+    // 32000] bf16 1 chunk 40.8 us against 3 chunks 43.6 us, fp32 2 chunks
+    // 79 us against 5 chunks 85 us; X1 [32768, 4096] bf16 8 chunks 41.1 us
+    // against 16 chunks 43.2 us, fp32 16 or 32 chunks alike.  Fewer chunks
+    // write fewer partials, and the blocks fill the CUs in one even round.
+    int64_t nchunk = 1;
+    if (base_blocks < cus && r >= 64) {
+        nchunk = (cus + base_blocks / 2) / base_blocks;
+        const int64_t max_chunks = r / 32;  // keep >= 32 rows per chunk
+        if (nchunk > max_chunks) nchunk = max_chunks > 1 ? max_chunks : 1;
+        if (nchunk > 65535) nchunk = 65535;
+    }
+    sp.chunk = (r + nchunk - 1) / nchunk;
+    sp.nchunk = (r + sp.chunk - 1) / sp.chunk;
+    if (sp.nchunk > 1) sp.partial_floats = outer * sp.nchunk * inner;
+    return sp;
+}
+
 template <typename T, int OP>
 void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const void* xv,
                   void* outv, const Scratch& scratch) {
@@ -652,34 +713,21 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     constexpr int N = Packet<T>::N;
     if (inner == 1) {
         const bool vec = r % N == 0 && aligned16(x);
-        // Fewer rows than fill the chip, and long ones: split each row into
-        // segments of at least 4096 elements, about two blocks per CU in
-        // all, and fold the partials in the same launch.  Measured on a
-        // whole 4096^2 float32 tensor: 11.7 us with two blocks per CU,
-        // against 11.9 (four), 13.0 (eight) and 12.8 (one).
-        if (outer < cus * 16 && r >= 8192) {
-            int64_t nseg = (cus * 2 + outer - 1) / outer;
-            const int64_t max_seg = r / 4096;  // >= 2 here
-            if (nseg > max_seg) nseg = max_seg;
-            int64_t chunk = (r + nseg - 1) / nseg;
-            if (vec) chunk = (chunk + N - 1) / N * N;
-            nseg = (r + chunk - 1) / chunk;
-            if (nseg > 1) {
-                const int64_t ngroups = (nseg + kFoldGroup - 1) / kFoldGroup;
-                TP_AMD_CHECK(outer <= kMaxFoldRows && outer * ngroups <= kMaxFoldGroups,
-                             "row reduction: ", outer, " rows of ", nseg, " segments exceed the arrival counters");
-                const int64_t nsegs = outer * nseg;
-                Partials partial(scratch, nsegs, device);
-                if (vec) {
-                    reduce_rows_fused_kernel<T, OP, true><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
-                        x, out, partial.get(), r, chunk, nseg, ngroups);
-                } else {
-                    reduce_rows_fused_kernel<T, OP, false><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
-                        x, out, partial.get(), r, chunk, nseg, ngroups);
-                }
-                TP_AMD_HIP_CHECK(hipGetLastError());
-                return;
+        const SplitPlan sp = plan_split(outer, r, 1, cus, N, vec, 0);
+        if (sp.nseg > 1) {
+            TP_AMD_CHECK(outer <= kMaxFoldRows && outer * sp.ngroups <= kMaxFoldGroups,
+                         "row reduction: ", outer, " rows of ", sp.nseg, " segments exceed the arrival counters");
+            const int64_t nsegs = outer * sp.nseg;
+            Partials partial(scratch, sp.partial_floats, device);
+            if (vec) {
+                reduce_rows_fused_kernel<T, OP, true><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                    x, out, partial.get(), r, sp.chunk, sp.nseg, sp.ngroups);
+            } else {
+                reduce_rows_fused_kernel<T, OP, false><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                    x, out, partial.get(), r, sp.chunk, sp.nseg, sp.ngroups);
             }
+            TP_AMD_HIP_CHECK(hipGetLastError());
+            return;
         }
         // One segment per row.  Four waves share a row of 4096 elements or
         // more; amax / amin of 16-bit storage (integer keys) run best one
@@ -709,28 +757,9 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     // Column reductions.
     const bool vec = inner % N == 0 && aligned16(x);
     const int64_t cols_per_block = vec ? col_lanes<T, true>() * N : col_lanes<T, false>();
-    const int64_t bx = (inner + cols_per_block - 1) / cols_per_block;
-    const int64_t z = outer < 65535 ? outer : 65535;
-    const int64_t base_blocks = bx * z;
-    // About one block per CU, each with eight 16-byte loads per thread in
-    // flight: nchunk = round(CUs / column ranges).  Measured on config 3's
-    // dim-0 reductions against the earlier two blocks per CU: X2 [4096,
-    // 32000] bf16 1 chunk 40.8 us against 3 chunks 43.6 us, fp32 2 chunks
-    // 79 us against 5 chunks 85 us; X1 [32768, 4096] bf16 8 chunks 41.1 us
-    // against 16 chunks 43.2 us, fp32 16 or 32 chunks alike.  Fewer chunks
-    // write fewer partials, and the blocks fill the CUs in one even round.
-    const int64_t target_blocks = cus;
-    int64_t nchunk = 1;
-    if (base_blocks < target_blocks && r >= 64) {
-        nchunk = (target_blocks + base_blocks / 2) / base_blocks;
-        const int64_t max_chunks = r / 32;  // keep >= 32 rows per chunk
-        if (nchunk > max_chunks) nchunk = max_chunks > 1 ? max_chunks : 1;
-        if (nchunk > 65535) nchunk = 65535;
-    }
-    const int64_t chunk = (r + nchunk - 1) / nchunk;
-    nchunk = (r + chunk - 1) / chunk;
-    const dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(nchunk),
-                    static_cast<unsigned>(z));
+    const SplitPlan sp = plan_split(outer, r, inner, cus, N, vec, cols_per_block);
+    const int64_t bx = sp.bx, nchunk = sp.nchunk, chunk = sp.chunk;
+    const dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(nchunk), static_cast<unsigned>(sp.z));
     if (nchunk == 1) {
         if (vec) {
             reduce_cols_kernel<T, T, OP, true, false>
@@ -746,7 +775,7 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
     // per column range always fits.
     TP_AMD_CHECK(outer * bx <= kMaxColCounters, "column reduction: ", outer * bx,
                  " column ranges exceed the arrival counters");
-    Partials partials(scratch, outer * nchunk * inner, device);
+    Partials partials(scratch, sp.partial_floats, device);
     float* partial = partials.get();
     // One launch: the last block of each column range folds the partials.
     if (vec) {
@@ -840,6 +869,24 @@ int tp_amd_launch_reduce_noalloc(int device, int op, int dtype, int64_t outer, i
 
 size_t tp_amd_reduce_noalloc_scratch_bytes(void) {
     return static_cast<size_t>(kScratchFloats) * sizeof(float);
+}
+
+int64_t tp_amd_reduce_partial_bytes(int compute_units, int dtype, int64_t outer, int64_t r, int64_t inner) {
+    int64_t esize = 0;
+    switch (dtype) {
+        case TP_AMD_FLOAT32: esize = 4; break;
+        case TP_AMD_BFLOAT16:
+        case TP_AMD_FLOAT16: esize = 2; break;
+        default: return -1;
+    }
+    if (compute_units <= 0 || outer < 0 || r < 0 || inner < 0) return -1;
+    if (outer == 0 || inner == 0 || r == 0) return 0;
+    const int64_t packet = 16 / esize;
+    const bool vec = (inner == 1 ? r : inner) % packet == 0;
+    // col_lanes: 16 lanes of 16-bit packets, 64 lanes of float32 packets or single elements
+    const int64_t cols_per_block = vec ? (esize == 2 ? 16 : 64) * packet : 64;
+    return plan_split(outer, r, inner, compute_units, packet, vec, cols_per_block).partial_floats *
+           static_cast<int64_t>(sizeof(float));
 }
 
 }  // extern "C"

@@ -381,6 +381,13 @@ int tp_amd_mem_get_info(int index, size_t* free_bytes, size_t* total_bytes) {
     });
 }
 
+int tp_amd_compute_units(int index, int* units) {
+    return guarded([&] {
+        TP_AMD_CHECK(units != nullptr, "tp_amd_compute_units: null output");
+        *units = cu_count(resolve_device(index));
+    });
+}
+
 int tp_amd_copy_bytes(void* dst, int dst_device, const void* src, int src_device,
                       size_t nbytes) {
     return guarded([&] {

@@ -11,7 +11,7 @@ from . import _library
 from .tensor import check
 
 __all__ = [
-    "current_device", "device", "device_count", "empty_cache", "is_available",
+    "compute_units", "current_device", "device", "device_count", "empty_cache", "is_available",
     "is_initialized", "max_memory_allocated", "max_memory_reserved", "mem_get_info",
     "memory_allocated", "memory_reserved", "memory_stats", "reset_peak_memory_stats",
     "set_device", "synchronize",
@@ -105,3 +105,10 @@ def mem_get_info(device=None) -> tuple[int, int]:
     free, total = ctypes.c_size_t(), ctypes.c_size_t()
     check(_library().tp_amd_mem_get_info(_index(device), ctypes.byref(free), ctypes.byref(total)))
     return free.value, total.value
+
+
+def compute_units(device=None) -> int:
+    """The device's compute units (what the kernels size their grids by)."""
+    units = ctypes.c_int()
+    check(_library().tp_amd_compute_units(_index(device), ctypes.byref(units)))
+    return units.value
