@@ -19,6 +19,9 @@ struct GemmArgs {
     void* c;
     int64_t ldc, stride_c;
     bool trans_a, trans_b;
+    // C stored transposed: element (i, j) of the product at c + j ldc + i
+    // (gemm_mfma_kernel only; set by the dispatch when it computes C^T).
+    bool trans_c = false;
 };
 
 // Any shape, stride and alignment (gemm.hip).

@@ -405,6 +405,35 @@ def test_mm_skinny_odd_k(dev, ops, orc, dtype):
     check(orc, got, exact(orc, dy, w, dtype), dtype, "skinny odd K")
 
 
+@pytest.mark.parametrize("m,n,k,pad", [(1664, 1408, 520, 0), (1701, 1300, 776, 1)], ids=["aligned", "odd-M-ldc"])
+def test_fp32_nn_as_transposed_product(amd, dev, ops, orc, m, n, k, pad):
+    """float32 A [M, K] @ B [K, N] with enough tiles to fill the GPU runs as
+    C^T = B^T A^T with C written transposed: ragged M and N, addmm's bias,
+    a full Cin with beta = 2 through the kernel ABI into a C whose rows are
+    ldc = N + pad apart (pad 1: rows not 16-byte aligned, element stores;
+    the pad column must stay untouched), and a batch of two."""
+    lib = amd.load()
+    a, b = sample(orc, (m, k), F32, 31, k ** -0.5), sample(orc, (k, n), F32, 32)
+    da, db = dev.from_numpy(a), dev.from_numpy(b)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    check(orc, ops.mm(da, db).numpy(), want, F32, "mm")
+    bias = sample(orc, (n,), F32, 33)
+    check(orc, ops.addmm(dev.from_numpy(bias), da, db, beta=0.5, alpha=2.0).numpy(),
+          2.0 * want + 0.5 * bias.astype(np.float64), F32, "addmm")
+    cin = sample(orc, (m, n), F32, 34)
+    ldc = n + pad
+    out = dev.from_numpy(np.full((m, ldc), 7.0, np.float32))
+    st = lib.tp_amd_launch_gemm(0, F32, 1, m, n, k, 0.5, da.data_ptr, k, 0, 0, db.data_ptr, n, 0, 0, 2.0,
+                                dev.from_numpy(cin).data_ptr, n, 1, 0, out.data_ptr, ldc, 0)
+    assert st == 0, lib.tp_mlu_last_error()
+    got = out.numpy()
+    assert np.all(got[:, n:] == 7.0), "the pad column was written"
+    check(orc, np.ascontiguousarray(got[:, :n]), 0.5 * want + 2.0 * cin.astype(np.float64), F32, "full Cin")
+    x, y = sample(orc, (2, m, k), F32, 35, k ** -0.5), sample(orc, (2, k, n), F32, 36)
+    check(orc, ops.bmm(dev.from_numpy(x), dev.from_numpy(y)).numpy(),
+          np.matmul(x.astype(np.float64), y.astype(np.float64)), F32, "bmm")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
 def test_mm_2047_cube(dev, ops, orc, dtype):
     """mm 2047^3 (odd everything) through ops.mm, checked on sampled
