@@ -285,6 +285,11 @@ def suite_gemm(ops, dev, ev):
         a, b = put((K, K), dtype, K ** -0.25), put((K, K), dtype, K ** -0.25)
         bias = put((K,), dtype, 1.0)
         at = ops.contiguous(a.t())
+        # the clock settles over the first products of a dtype (float32
+        # 4096^3 runs ~15 % slower for its first ten or so): ten untimed
+        # products before the dtype's first row
+        for _ in range(10):
+            ops.mm(a, b)
         record("mm_4096", lambda: ops.mm(a, b), 2 * K ** 3, dtype)
         record("addmm_4096", lambda: ops.addmm(bias, a, b), 2 * K ** 3, dtype)
         record("mm_4096_At", lambda: ops.mm(at.t(), b), 2 * K ** 3, dtype)
