@@ -98,7 +98,7 @@ def test_blocks_set_aside_until_reset(dev, ops, graph_mod, runtime):
     y = ops.mul_scalar(x, 2.0)                   # eager work cannot take either block
     g.replay()
     runtime.synchronize()
-    assert np.allclose(g._outputs.numpy(), np.exp(0.5), rtol=1e-6)
+    assert np.allclose(g.results.numpy(), np.exp(0.5), rtol=1e-6)
     assert np.array_equal(y.numpy(), np.full((1024, 1024), 2.0, np.float32))
     g.reset()                                    # result released, blocks returned
     assert g.stats()[1] == 0
