@@ -17,7 +17,8 @@ import importlib
 import numpy as np
 import pytest
 
-from _check import BF16, F16, F32, assert_bitexact, assert_elementwise, assert_normwise
+from _check import (BF16, F16, F32, as_float, assert_bitexact, assert_elementwise, assert_normwise,
+                    assert_pointwise)
 
 pytestmark = pytest.mark.gpu
 
@@ -95,6 +96,38 @@ def test_layer_norm_backward(dev, ops, orc, dtype, shape, norm):
     ox2, _, ob2 = orc.layer_norm_backward(dtype, dy, x, D, m, r, None)
     assert_normwise(gx2.numpy(), ox2, dtype, 1, "dx without weight")
     assert_normwise(gb2.numpy().reshape(-1), ob2, dtype, scale, "dbias without weight")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+def test_layer_norm_bench_shape(dev, ops, orc, dtype):
+    """[8192, 4096], the shape bench.py times: every CU holds a block of the
+    backward's rows kernel, so the fold adds 256 partial rows a column (its
+    full 16-load batches), which the smaller cases above never reach."""
+    shape, norm, D = (8192, 4096), (4096,), 4096
+    x = sample(orc, shape, dtype, 11, 1.5, -0.25)
+    w = sample(orc, norm, dtype, 12)
+    b = sample(orc, norm, dtype, 13)
+    dy = sample(orc, shape, dtype, 14)
+    dx_, w_, b_ = (dev.from_numpy(a, dtype=dtype) for a in (x, w, b))
+    y, mean, rstd = ops.native_layer_norm(dx_, norm, w_, b_, eps=1e-5)
+    wy, _, _ = orc.layer_norm(dtype, x, D, w, b, 1e-5)
+    assert_normwise(y.numpy(), wy, dtype, 1, "y")
+    m, r = mean.numpy(), rstd.numpy()
+    gx, gw, gb = ops.native_layer_norm_backward(dev.from_numpy(dy, dtype=dtype), dx_, norm, mean,
+                                                rstd, w_, b_)
+    ox, ow, ob = orc.layer_norm_backward(dtype, dy, x, D, m, r, w)
+    assert_normwise(gx.numpy(), ox, dtype, 1, "dx")
+    scale = float(np.sqrt(shape[0]))
+    assert_normwise(gw.numpy(), ow, dtype, scale, "dweight")
+    assert_normwise(gb.numpy(), ob, dtype, scale, "dbias")
+    # Per column: a float32 sum of `rows` terms is within (rows + 2) u sum|term|
+    # of the exact sum (u = 2^-24), plus 3 u per term for xhat and the product.
+    xf = as_float(x, dtype).astype(np.float64)
+    dyf = as_float(dy, dtype).astype(np.float64)
+    xhat = (xf - m.astype(np.float64)[:, None]) * r.astype(np.float64)[:, None]
+    u, rows = 2.0 ** -24, shape[0]
+    assert_pointwise(gw.numpy(), ow, dtype, (rows + 5) * u * np.abs(dyf * xhat).sum(axis=0), "dweight per column")
+    assert_pointwise(gb.numpy(), ob, dtype, (rows + 2) * u * np.abs(dyf).sum(axis=0), "dbias per column")
 
 
 def test_layer_norm_strided_input_and_declines(dev, ops, orc):
