@@ -31,7 +31,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,gemm,gemm32,linear,bmm,reduce,reduce_all,softmax,nn,mlp,odd}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,bmm,reduce,reduce_all,softmax,nn,mlp,odd}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -883,6 +883,10 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              row-major; B transposed; A transposed; both transposed), the
              four layouts twice over (the second pass at a settled clock);
     gemm32:  the same in float32, five products a layout;
+    linear:  ten config-4 bf16 linears, x [8192, 4096] @ W[11008, 4096]^T + b;
+    vs_torch: bf16 4096^3 A @ B and A @ B^T and the config-4 linear, from
+             this library and from torch (hipBLASLt) on the same GPU,
+             interleaved: four rounds of ten calls a case each;
     mlp:     three config-5b training steps (fp32 MLP, batch 8192, four
              Linear(4096, 4096) + ReLU, Linear(4096, 1000), log_softmax, NLL
              through mul + sum, backward, SGD) after one untimed step;
@@ -967,6 +971,37 @@ def profile_launches(what: str, lib, ops, dev) -> None:
         bias = ops.to(dev.from_numpy(g.standard_normal(11008, dtype=np.float32)), BF16)
         for _ in range(10):
             ops.linear(x, w, bias)
+    elif what == "vs_torch":
+        # The bf16 products of config 4 from this library and from torch on
+        # the same GPU (hipBLASLt), interleaved: per round and case, ten
+        # calls of one then ten of the other, the order swapped every round.
+        import torch
+        F = torch.nn.functional
+        g = np.random.default_rng(0)
+
+        def both(shape):
+            a32 = g.standard_normal(shape, dtype=np.float32) * np.float32(shape[-1] ** -0.25)
+            return ops.to(dev.from_numpy(a32), BF16), torch.from_numpy(a32).to("cuda").to(torch.bfloat16)
+
+        a, ta = both((4096, 4096))
+        b, tb = both((4096, 4096))
+        x, tx = both((8192, 4096))
+        w, tw = both((11008, 4096))
+        bias, tbias = both((11008,))
+        cases = [(lambda: ops.mm(a, b), lambda: torch.mm(ta, tb)),
+                 (lambda: ops.mm(a, b.t()), lambda: torch.mm(ta, tb.t())),
+                 (lambda: ops.linear(x, w, bias), lambda: F.linear(tx, tw, tbias))]
+
+        def drain():
+            assert lib.tp_amd_synchronize(0) == 0
+            torch.cuda.synchronize()
+
+        for rnd in range(4):
+            for ours, theirs in cases:
+                for fn in ((ours, theirs) if rnd % 2 == 0 else (theirs, ours)):
+                    for _ in range(10):
+                        fn()
+                    drain()
     elif what == "reduce":
         g = np.random.default_rng(0)
         for shape in ((32768, 4096), (4096, 32000)):
@@ -1070,8 +1105,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "bmm", "reduce", "reduce_all",
-                                         "softmax", "nn", "mlp", "odd"],
+    p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "vs_torch", "bmm",
+                                         "reduce", "reduce_all", "softmax", "nn", "mlp", "odd"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
@@ -1079,6 +1114,13 @@ def main() -> int:
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         return 2
 
+    if args.profile == "vs_torch":
+        # torch's GPU path loads its own copy of the HIP runtime by a name
+        # this library does not ask for; loaded first, it is the one copy in
+        # the process, and this library binds to it by soname.  Loaded after
+        # this library, the process would hold two runtimes on one GPU.
+        import torch
+        torch.cuda.init()
     lib = amd.load()
     ops = importlib.import_module("tensorplay-mlu_amd.ops")
     runtime = importlib.import_module("tensorplay-mlu_amd.runtime")
