@@ -3,11 +3,11 @@
 // tensorplay_mlu/csrc/ReduceKernels.cpp:21-44).
 //
 // * inner == 1 (row reductions): a wavefront (or, for long rows, a whole
-//   256-thread block) reduces one row segment with 16-byte packet loads,
-//   then combines across lanes with DPP/shuffle steps and across waves in
-//   LDS.  When there are too few rows to fill 256 CUs (a whole-tensor sum),
-//   rows are split into segments of one block each, and the last block of a
-//   row to finish folds the row's float32 partials in the same launch.
+//   block) reduces one row segment with 16-byte packet loads, then combines
+//   across lanes with DPP/shuffle steps and across waves in LDS.  When there
+//   are too few rows to fill 256 CUs (a whole-tensor sum), rows are split
+//   into segments of one block each, and the last block of a row to finish
+//   folds the row's float32 partials in the same launch.
 // * inner > 1 (column reductions, e.g. dim 0 of [32768, 4096]): lanes walk
 //   the contiguous inner axis with packets, four row groups per block share
 //   the rows of a chunk, and chunks of rows are spread over the grid; the
@@ -276,17 +276,17 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
     }
 }
 
-// The block's value of `v` (combined over its waves in wave order), in
-// thread 0.
-template <int OP>
+// The value of `v` over a block of BLOCK threads (combined over its waves
+// in wave order), in thread 0.
+template <int OP, int BLOCK = kBlock>
 __device__ __forceinline__ float block_reduce(float v) {
-    __shared__ float waves[kBlock / kWave];
+    __shared__ float waves[BLOCK / kWave];
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     v = lane_reduce<OP>(v);
     if (lane == 0) waves[wave] = v;
     __syncthreads();
     if (wave == 0) {
-        v = lane < kBlock / kWave ? waves[lane] : Combine<OP>::identity();
+        v = lane < BLOCK / kWave ? waves[lane] : Combine<OP>::identity();
         v = lane_reduce<OP>(v);
     }
     return v;
@@ -300,8 +300,8 @@ __device__ __forceinline__ float block_reduce(float v) {
 constexpr int kCounterStride = 32;  // uint32 slots per 128-byte line
 
 // Few long rows (a whole-tensor sum, a loss over all logits): each row is
-// split into nseg segments, one 256-thread block a segment, and the partials
-// are folded in the same launch.  Block s reduces segment s (row s / nseg,
+// split into nseg segments, one block of fused_threads() a segment, and the
+// partials are folded in the same launch.  Block s reduces segment s (row s / nseg,
 // elements [(s % nseg) * chunk, +chunk)), stores its float32 partial with an
 // agent-coherent store, waits for the store to complete, and counts its
 // arrival on its group's counter (kFoldGroup consecutive segments of the
@@ -309,7 +309,7 @@ constexpr int kCounterStride = 32;  // uint32 slots per 128-byte line
 // has several groups, each group's last arrival then counts the group on the
 // row's counter.  The row's last arrival reads all nseg partials back with
 // agent-coherent loads and folds them in a fixed order (thread t takes
-// partials t, t + 256, ... in turn, then the block combines its lanes and
+// partials t, t + blockDim, ... in turn, then the block combines its lanes and
 // waves in order), so the bits do not depend on which block came last, and
 // writes the result.  Each counter is reset by its last arrival for the next
 // launch (device globals start zeroed when the code object loads).
@@ -331,8 +331,21 @@ constexpr int64_t kMaxFoldRows = 4096;
 __device__ unsigned int group_counters[kMaxFoldGroups * kCounterStride];
 __device__ unsigned int row_counters[kMaxFoldRows * kCounterStride];
 
-template <typename Tin, int OP, bool VEC>
-__global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
+// Threads of a fused-fold block, and such blocks a CU (segments_per_cu):
+// 1024 threads a CU either way.  Measured on whole 4096^2 tensors, averages of
+// 20 calls back to back: float32 sum 10.5 us as two 512-thread blocks a CU,
+// against 10.8 (two of 256), 11.9 (one of 512 or of 1024), 11.3 (four of
+// 256); bf16 sum 5.7 us as one 1024-thread block, 5.7 (two of 512), 5.9 (one
+// of 512), 6.1 (two of 256), 6.7 (two of 1024); bf16 amax 6.0-6.1 us as one
+// 1024-thread block against 6.5 (two of 256).
+template <typename Tin>
+constexpr int fused_threads() {
+    return sizeof(typename Elem<Tin>::storage) == 4 ? 512 : 1024;
+}
+constexpr int64_t segments_per_cu(int64_t packet) { return packet == 4 ? 2 : 1; }
+
+template <typename Tin, int OP, bool VEC, int BLOCK = fused_threads<Tin>()>
+__global__ __launch_bounds__(BLOCK) void reduce_rows_fused_kernel(
     const typename Elem<Tin>::storage* x, typename Elem<Tin>::storage* out, float* partial,
     int64_t r, int64_t chunk, int64_t nseg, int64_t ngroups) {
     constexpr int N = VEC ? Packet<Tin>::N : 1;
@@ -352,17 +365,17 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
         constexpr bool kNt = sizeof(typename Elem<Tin>::storage) == 4;
         const int64_t pb = begin / N, pe = end / N;
         if constexpr (kMinMax<OP>) {
-            acc = row_keys<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
-            if (acc != acc) acc = row_exact<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
+            acc = row_keys<Tin, OP, BLOCK, 8, kNt>(p, pb, pe, tid);
+            if (acc != acc) acc = row_exact<Tin, OP, BLOCK, 8, kNt>(p, pb, pe, tid);
         } else {
-            acc = row_exact<Tin, OP, kBlock, 8, kNt>(p, pb, pe, tid);
+            acc = row_exact<Tin, OP, BLOCK, 8, kNt>(p, pb, pe, tid);
         }
     } else {
-        for (int64_t j = begin + tid; j < end; j += kBlock) {
+        for (int64_t j = begin + tid; j < end; j += BLOCK) {
             acc = Combine<OP>::apply(acc, Elem<Tin>::load(p[j]));
         }
     }
-    acc = block_reduce<OP>(acc);
+    acc = block_reduce<OP, BLOCK>(acc);
     // The block's group of segments, and that group's slot among the row's.
     const int64_t group = part / kFoldGroup;
     const int64_t first = group * kFoldGroup;
@@ -397,10 +410,10 @@ __global__ __launch_bounds__(kBlock) void reduce_rows_fused_kernel(
     // thread t taking partials t, t + 256, ...
     const float* q = partial + row * nseg;
     float v = Combine<OP>::identity();
-    for (int64_t k = tid; k < nseg; k += kBlock) {
+    for (int64_t k = tid; k < nseg; k += BLOCK) {
         v = Combine<OP>::apply(v, __hip_atomic_load(q + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
-    v = block_reduce<OP>(v);
+    v = block_reduce<OP, BLOCK>(v);
     if (tid == 0) out[row] = Elem<Tin>::store(finish<OP>(v, r, true));
 }
 
@@ -661,10 +674,9 @@ SplitPlan plan_split(int64_t outer, int64_t r, int64_t inner, int64_t cus, int64
                      int64_t cols_per_block) {
     SplitPlan sp;
     if (inner == 1) {
-        // Measured on a whole 4096^2 float32 tensor: 11.7 us with two blocks
-        // per CU, against 11.9 (four), 13.0 (eight) and 12.8 (one).
+        // About segments_per_cu(packet) blocks a CU (above).
         if (outer < cus * 16 && r >= 8192) {
-            int64_t nseg = (cus * 2 + outer - 1) / outer;
+            int64_t nseg = (cus * segments_per_cu(packet) + outer - 1) / outer;
             const int64_t max_seg = r / 4096;  // >= 2 here
             if (nseg > max_seg) nseg = max_seg;
             int64_t chunk = (r + nseg - 1) / nseg;
@@ -720,10 +732,10 @@ void reduce_typed(int device, int64_t outer, int64_t r, int64_t inner, const voi
             const int64_t nsegs = outer * sp.nseg;
             Partials partial(scratch, sp.partial_floats, device);
             if (vec) {
-                reduce_rows_fused_kernel<T, OP, true><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                reduce_rows_fused_kernel<T, OP, true><<<static_cast<unsigned>(nsegs), fused_threads<T>(), 0, st>>>(
                     x, out, partial.get(), r, sp.chunk, sp.nseg, sp.ngroups);
             } else {
-                reduce_rows_fused_kernel<T, OP, false><<<static_cast<unsigned>(nsegs), kBlock, 0, st>>>(
+                reduce_rows_fused_kernel<T, OP, false><<<static_cast<unsigned>(nsegs), fused_threads<T>(), 0, st>>>(
                     x, out, partial.get(), r, sp.chunk, sp.nseg, sp.ngroups);
             }
             TP_AMD_HIP_CHECK(hipGetLastError());

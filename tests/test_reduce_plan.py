@@ -28,6 +28,8 @@ def test_exact_figures(lib):
     q = lib.tp_amd_reduce_partial_bytes
     # whole 2^24-element float32 tensor: 512 segments of 32768 (two blocks a CU)
     assert q(256, F32, 1, 1 << 24, 1) == 512 * 4
+    # whole 4096^2 bf16 tensor: 256 segments of 65536 (one block a CU)
+    assert q(256, BF16, 1, 4096 * 4096, 1) == 256 * 4
     # [32768, 4096] float32 over dim 0: 16 column ranges of 256 -> 16 chunks of 2048 rows
     assert q(256, F32, 1, 32768, 4096) == 16 * 4096 * 4
     # [4096, 32000] bf16 over dim 0: 250 ranges of 128 columns -> one chunk, no partials
