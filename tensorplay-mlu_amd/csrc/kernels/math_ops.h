@@ -4,15 +4,17 @@
 //
 // Two precisions of the transcendental functions, chosen by the storage
 // dtype (FAST = 16-bit storage):
-//   * float32 storage: ROCm's device math library (expf, logf, erfcf, tanhf,
-//     powf), accurate to an ulp or two;
+//   * float32 storage: ROCm's device math library (expf, logf, tanhf, powf),
+//     accurate to an ulp or two, except the normal CDF and density of gelu's
+//     erf form and its backward (normal_f32 below: a few ulps, at HBM speed);
 //   * bfloat16 / float16 storage, where the result keeps 8 or 11 significant
 //     bits and the library functions' instruction count, not HBM, would set
 //     the pace: the hardware v_exp_f32 / v_log_f32 / v_sqrt_f32 / v_rcp_f32
 //     and, for the normal CDF, the Chebyshev-fitted erfc of Numerical Recipes
 //     in C (2nd ed., section 6.2, "erfcc": relative error below 1.2e-7 for
 //     every argument).  Their float32 errors (a few 1e-7 relative) move a
-//     16-bit result by at most one unit in its last place.
+//     16-bit result by at most one unit in its last place, which the GPU
+//     tests check at every finite 16-bit input.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,11 +31,37 @@ constexpr float kGeluTanhC = 0.044715f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+// 1 / (1 + e^-x) from e = e^-|x| <= 1: for x < 0 it is e / (1 + e), so the
+// exponential never overflows and a sigmoid far below 1 keeps its value
+// (1 / (1 + inf) would give 0 below x = -88.7, where the result is a float32
+// subnormal).
+__device__ __forceinline__ float sigmoidf(float x) {
+    const float e = expf(-fabsf(x));
+    const float r = 1.0f / (1.0f + e);
+    return x >= 0.0f ? r : e * r;
+}
 
 // ---- fast forms (16-bit storage) ------------------------------------------------
+//
+// v_exp_f32 returns 0 for results below 2^-126, where bfloat16 (float32's
+// exponent range) still has subnormal values, and v_sqrt_f32 reads a
+// subnormal input as 0 (both measured over every bfloat16 value).
 
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+// e^x as (2^(a/2))^2, a = x log2 e: the halves stay normal down to a = -252
+// and their product underflows gradually.  One multiply and about one
+// float32 ulp more than 2^a alone, where a select between a raised and a
+// plain argument cost five instructions (bfloat16 gelu 46 -> 59 us).
+__device__ __forceinline__ float exp_fast(float x) {
+    const float h = __builtin_amdgcn_exp2f(x * (0.5f * kLog2e));
+    return h * h;
+}
+
+// sqrt on v_sqrt_f32, a subnormal x scaled by 2^32 first and the root by 2^-16 after.
+__device__ __forceinline__ float sqrt_fast(float x) {
+    const bool tiny = x < 0x1p-126f;
+    const float r = __builtin_amdgcn_sqrtf(tiny ? x * 0x1p32f : x);
+    return tiny ? r * 0x1p-16f : r;
+}
 
 // ln x on v_log_f32 (log2); subnormal inputs are scaled into the normal range
 // first, so they are not flushed.
@@ -43,14 +71,16 @@ __device__ __forceinline__ float log_fast(float x) {
     return (tiny ? l - 24.0f : l) * kLn2;
 }
 
+// sigmoidf's form on the hardware exponential and reciprocal.
 __device__ __forceinline__ float sigmoid_fast(float x) {
-    return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x));
+    const float e = exp_fast(-fabsf(x));
+    const float r = __builtin_amdgcn_rcpf(1.0f + e);
+    return x >= 0.0f ? r : e * r;
 }
 
-// erfc(z) for z >= 0: t exp(-z^2 + P(t)), t = 1 / (1 + z/2), P the degree-9
-// Chebyshev fit of Numerical Recipes' erfcc.
-__device__ __forceinline__ float erfc_pos_fast(float z) {
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+// P(t) of erfc(z) = t exp(-z^2 + P(t)), t = 1 / (1 + z/2), z >= 0: the
+// degree-9 Chebyshev fit of Numerical Recipes' erfcc.
+__device__ __forceinline__ float erfc_fit(float t) {
     float p = 0.17087277f;
     p = fmaf(p, t, -0.82215223f);
     p = fmaf(p, t, 1.48851587f);
@@ -60,15 +90,16 @@ __device__ __forceinline__ float erfc_pos_fast(float z) {
     p = fmaf(p, t, 0.09678418f);
     p = fmaf(p, t, 0.37409196f);
     p = fmaf(p, t, 1.00002368f);
-    p = fmaf(p, t, -1.26551223f);
-    return t * exp_fast(fmaf(-z, z, p));
+    return fmaf(p, t, -1.26551223f);
 }
 
-// Normal CDF Phi(x) = erfc(-x / sqrt(2)) / 2.
+// Normal CDF Phi(x) = erfc(-x / sqrt(2)) / 2 on the hardware exponential.
 __device__ __forceinline__ float phi_fast(float x) {
-    const float z = x * 0.70710678118654752440f;  // -(-x / sqrt 2)
-    const float c = erfc_pos_fast(fabsf(z));      // erfc(|z|)
-    return 0.5f * (z >= 0.0f ? 2.0f - c : c);
+    const float z = x * kSqrt1_2;  // -(-x / sqrt 2)
+    const float az = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, az, 1.0f));
+    const float c = t * exp_fast(fmaf(-az, az, erfc_fit(t)));  // erfc(|z|)
+    return z >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
 }
 
 // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
@@ -79,8 +110,47 @@ __device__ __forceinline__ float gelu_tanhf(float x) {
     return x * sigmoidf(2.0f * u);
 }
 
-// x Phi(x) = 0.5 x erfc(-x / sqrt(2)).
-__device__ __forceinline__ float gelu_erff(float x) { return 0.5f * x * erfcf(-x * kSqrt1_2); }
+// The normal CDF Phi(x) for float32 storage and, with WANT_PDF, the density
+// phi(x) in *pdf.  The library form 0.5 erfc(-x / sqrt 2) loses accuracy
+// before erfcf runs: rounding z = x / sqrt 2 to float32 moves erfc(z) by
+// 2 z^2 times z's relative error (14-23 ulps at 1 <= |x| < 5, ~200 at
+// |x| > 8), and erfcf's instruction count made float32 gelu compute-bound.
+// Here z = zh + zlo with zlo the rounding error of zh (1/sqrt 2 carried to
+// 48 bits), and erfc(z) = t exp(-z^2 + P(t)) with the erfcc fit above:
+// z^2 = zz + zl exactly (zz = zh^2 rounded, zl its rounding error plus
+// 2 zh zlo), e^-zz is reduced by n ln 2 (Cody and Waite: n = rint(-zz
+// log2 e); ln 2 split so that n ln2_hi is exact for |n| < 2^12) and the
+// small rest, r - zl + P(t), goes to v_exp_f32 and v_ldexp_f32.  The density
+// shares the reduction: phi(x) = e^(-z^2) / sqrt(2 pi).  Emulated in float64
+// against scipy.special.erfc over |x| <= 14: gelu within 9 ulps everywhere
+// (the library form: 14-200), the density within 3.  Measured on [8192,
+// 8192] float32: gelu 74.7-75.6 us against 88-98 us with erfcf, the
+// backward 133-139 us against 156-165 us (relu 72.6 us).
+template <bool WANT_PDF>
+__device__ __forceinline__ float normal_f32(float x, float* pdf) {
+    constexpr float kSqrt1_2Lo = 1.21016175e-08f;  // 1/sqrt(2) - kSqrt1_2
+    constexpr float kLn2Hi = 0.69311523f;          // ln 2 with 12 trailing zero bits
+    constexpr float kLn2Lo = 3.1946183e-05f;       // ln 2 - kLn2Hi
+    const float ax = fabsf(x);
+    const float zh = ax * kSqrt1_2;
+    const float zlo = fmaf(ax, kSqrt1_2, -zh) + ax * kSqrt1_2Lo;
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, zh, 1.0f));
+    const float p = erfc_fit(t);
+    // Beyond z = 10.5 erfc and the density are below float32's range (and an
+    // infinite z would make NaN of the reduction): both are 0 there.
+    const bool live = zh < 10.5f;
+    const float zs = live ? zh : 0.0f;
+    const float zz = zs * zs;
+    const float zl = fmaf(zs, zs, -zz) + 2.0f * zs * (live ? zlo : 0.0f);
+    const float n = rintf(-zz * kLog2e);
+    const float r = fmaf(-n, kLn2Lo, fmaf(-n, kLn2Hi, -zz));
+    const int ni = static_cast<int>(n);
+    const float c = live ? t * __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((r + (p - zl)) * kLog2e), ni) : 0.0f;
+    if constexpr (WANT_PDF) {
+        *pdf = live ? kInvSqrt2Pi * __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((r - zl) * kLog2e), ni) : 0.0f;
+    }
+    return x >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
+}
 
 template <int OP>
 struct BinaryFn;
@@ -114,7 +184,7 @@ struct UnaryFn {
     __device__ __forceinline__ float operator()(float x) const {
         if constexpr (OP == TP_AMD_UNARY_EXP) return FAST ? exp_fast(x) : expf(x);
         else if constexpr (OP == TP_AMD_UNARY_LOG) return FAST ? log_fast(x) : logf(x);
-        else if constexpr (OP == TP_AMD_UNARY_SQRT) return FAST ? __builtin_amdgcn_sqrtf(x) : sqrtf(x);
+        else if constexpr (OP == TP_AMD_UNARY_SQRT) return FAST ? sqrt_fast(x) : sqrtf(x);
         else if constexpr (OP == TP_AMD_UNARY_RSQRT) return 1.0f / sqrtf(x);
         else if constexpr (OP == TP_AMD_UNARY_NEG) return -x;
         else if constexpr (OP == TP_AMD_UNARY_ABS) return fabsf(x);
@@ -126,7 +196,7 @@ struct UnaryFn {
         else if constexpr (OP == TP_AMD_UNARY_SILU) {
             return FAST ? x * sigmoid_fast(x) : x / (1.0f + expf(-x));
         } else if constexpr (OP == TP_AMD_UNARY_GELU) {
-            return FAST ? x * phi_fast(x) : gelu_erff(x);
+            return x * (FAST ? phi_fast(x) : normal_f32<false>(x, nullptr));
         } else {
             if constexpr (FAST) {
                 const float u = kSqrt2OverPi * (x + kGeluTanhC * x * x * x);
@@ -153,10 +223,20 @@ struct BackwardFn {
         } else if constexpr (OP == TP_AMD_BACKWARD_TANH) {
             return g * (1.0f - s * s);
         } else if constexpr (OP == TP_AMD_BACKWARD_GELU) {
-            const float cdf = FAST ? phi_fast(s) : 0.5f * erfcf(-s * kSqrt1_2);
-            const float pdf = kInvSqrt2Pi * (FAST ? exp_fast(-0.5f * s * s) : expf(-0.5f * s * s));
+            float cdf, pdf;
+            if constexpr (FAST) {
+                cdf = phi_fast(s);
+                pdf = kInvSqrt2Pi * exp_fast(-0.5f * s * s);
+            } else {
+                cdf = normal_f32<true>(s, &pdf);
+            }
             return g * (cdf + s * pdf);
         } else if constexpr (OP == TP_AMD_BACKWARD_GELU_TANH) {
+            // Beyond |s| = 20 the derivative rounds to 1 (s > 0) or to 0
+            // (s < 0) in float32; s is held there so that s^2 and du stay
+            // finite (past |s| = 1.8e19, s^2 overflows and 0 * inf would give
+            // NaN).  A NaN s stays NaN.
+            s = fabsf(s) > 20.0f ? copysignf(20.0f, s) : s;
             const float x2 = s * s;
             const float u = kSqrt2OverPi * (s + kGeluTanhC * x2 * s);
             const float sg = sigmoid(2.0f * u);

@@ -217,6 +217,86 @@ def test_activations(dev, ops, orc, dtype):
     assert_bitexact(r.numpy(), orc.unary(8, dtype, a), "relu_")
 
 
+def test_gelu_erf_form_float32_sweep(dev, ops, orc):
+    """gelu (erf form) and its backward in float32 over a dense grid of
+    [-14, 14] and special values: the rtol 1e-5 bar everywhere, and gelu
+    within 16 ulps of the correctly rounded value wherever it is a normal
+    float (|x| <= 12), the bound the float32 normal CDF is built to (it keeps
+    the rounding error of x / sqrt 2, which a plain erfcf(-x / sqrt 2) drops:
+    ~200 ulps at |x| > 8)."""
+    x = np.concatenate([np.linspace(-14, 14, (1 << 20) + 1, dtype=np.float32),
+                        np.float32([0.0, -0.0, 1e-30, -1e-30, 1e30, -1e30])])
+    dx_ = up(dev, x, F32)
+    got = ops.gelu(dx_).numpy()
+    want = orc.unary(12, F32, x)
+    assert_elementwise(got, want, F32, "gelu")
+    normal = np.abs(x) <= 12
+    assert_elementwise(got[normal], want[normal], F32, "gelu, |x| <= 12", max_ulp=16)
+    assert np.array_equal(np.signbit(got[want == 0]), np.signbit(want[want == 0])), "signs of zero results"
+    ones = np.ones_like(x)
+    gb = ops.gelu_backward(up(dev, ones, F32), dx_).numpy()
+    assert_elementwise(gb, orc.activation_backward(3, F32, ones, x), F32, "gelu_backward")
+    # infinities and NaN: x Phi(x) is inf at +inf, NaN at -inf (-inf * 0) and NaN
+    special = np.float32([np.inf, -np.inf, np.nan])
+    got_s = ops.gelu(up(dev, special, F32)).numpy()
+    assert got_s[0] == np.inf and np.isnan(got_s[1]) and np.isnan(got_s[2])
+    assert np.array_equal(np.isnan(orc.unary(12, F32, special)), np.isnan(got_s))
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+def test_narrow_float_math_at_every_value(dev, ops, orc, dtype):
+    """Every transcendental unary op and activation backward at every finite
+    16-bit value, within one storage ulp of the oracle (NaN where it gives
+    NaN).  The backward ops take an upstream gradient of 1, so dx is the
+    derivative rounded once.  bfloat16 reaches float32's exponent range, so
+    this covers the subnormal results of exp, sigmoid, silu and both gelu
+    forms far out in their tails and sqrt of subnormal inputs."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    every = bits if dtype == BF16 else bits.view(np.float16)
+    a = every[np.isfinite(orc.to_float(every, dtype))]
+    d = up(dev, a, dtype)
+    one = orc.from_float(np.ones(a.shape, np.float32), dtype)
+    dg = up(dev, one, dtype)
+    y_sig, y_tanh = orc.unary(9, dtype, a), orc.unary(10, dtype, a)
+    cases = [("exp", ops.exp(d), orc.unary(0, dtype, a)),
+             ("log", ops.log(d), orc.unary(1, dtype, a)),
+             ("sqrt", ops.sqrt(d), orc.unary(2, dtype, a)),
+             ("rsqrt", ops.rsqrt(d), orc.unary(3, dtype, a)),
+             ("sigmoid", ops.sigmoid(d), y_sig),
+             ("tanh", ops.tanh(d), y_tanh),
+             ("silu", ops.silu(d), orc.unary(11, dtype, a)),
+             ("gelu", ops.gelu(d), orc.unary(12, dtype, a)),
+             ("gelu tanh", ops.gelu(d, "tanh"), orc.unary(13, dtype, a)),
+             ("sigmoid_backward", ops.sigmoid_backward(dg, up(dev, y_sig, dtype)),
+              orc.activation_backward(1, dtype, one, y_sig)),
+             ("tanh_backward", ops.tanh_backward(dg, up(dev, y_tanh, dtype)),
+              orc.activation_backward(2, dtype, one, y_tanh)),
+             ("gelu_backward", ops.gelu_backward(dg, d), orc.activation_backward(3, dtype, one, a)),
+             ("gelu_backward tanh", ops.gelu_backward(dg, d, "tanh"), orc.activation_backward(4, dtype, one, a)),
+             ("silu_backward", ops.silu_backward(dg, d), orc.activation_backward(5, dtype, one, a))]
+    for what, got, want in cases:
+        got = got.numpy()
+        nan_g, nan_w = np.isnan(orc.to_float(got, dtype)), np.isnan(orc.to_float(want, dtype))
+        assert np.array_equal(nan_g, nan_w), f"{what}: NaN at {int((nan_g != nan_w).sum())} inputs differs"
+        assert_elementwise(got[~nan_w], want[~nan_w], dtype, what)
+
+
+def test_math_tails_float32(dev, ops, orc):
+    """float32 tails: sigmoid and silu far below -88.7 (where 1 / (1 + e^-x)
+    would give 0 instead of a subnormal), and the tanh-form gelu derivative at
+    |x| up to 1e30 (where x^2 overflows float32), against the oracle; the
+    derivative must be finite there."""
+    x = np.concatenate([-np.geomspace(80.0, 110.0, 4001, dtype=np.float32),
+                        np.float32([1e19, -1e19, 2e19, -2e19, 1e30, -1e30, 3.4e38, -3.4e38])])
+    d = up(dev, x, F32)
+    assert_elementwise(ops.sigmoid(d).numpy(), orc.unary(9, F32, x), F32, "sigmoid", max_ulp=2)
+    assert_elementwise(ops.silu(d).numpy(), orc.unary(11, F32, x), F32, "silu")
+    ones = np.ones_like(x)
+    got = ops.gelu_backward(up(dev, ones, F32), d, "tanh").numpy()
+    assert np.isfinite(got).all(), "gelu tanh backward: NaN or inf"
+    assert_elementwise(got, orc.activation_backward(4, F32, ones, x), F32, "gelu_backward tanh")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_activation_backward(dev, ops, orc, dtype):
     x = sample(orc, (37, 29), dtype, 5)
