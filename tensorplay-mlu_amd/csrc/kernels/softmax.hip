@@ -37,8 +37,14 @@ constexpr int kBlock = 256;
 constexpr float kLog2e = 1.44269504088896340736f;
 
 // e^d on v_exp_f32 (the softmax arguments d = x - max are <= 0, where its
-// error stays within a few float32 ulps).
-__device__ __forceinline__ float exp_fast(float d) { return __builtin_amdgcn_exp2f(d * kLog2e); }
+// error stays within a few float32 ulps), as (2^(a/2))^2 with a = d log2 e:
+// the instruction returns 0 for results below 2^-126, where the halves are
+// still normal and their product underflows gradually, so an entry 88-103
+// below its row's maximum keeps its subnormal value (bfloat16 has them).
+__device__ __forceinline__ float exp_fast(float d) {
+    const float h = __builtin_amdgcn_exp2f(d * (0.5f * kLog2e));
+    return h * h;
+}
 
 __device__ __forceinline__ float wave_max(float v) {
     return wave_allreduce(v, [](float a, float b) { return fmaxf(a, b); });

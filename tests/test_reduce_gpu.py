@@ -315,6 +315,37 @@ def test_softmax_nan_over_a_leading_axis(dev, ops, orc, dtype, shape, dim):
                                 yh, g, outer, size, inner, f"backward log={log}")
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape,dim", [((64, 1000), -1), ((40, 16400), -1), ((6, 70000), -1),
+                                       ((300, 130), 0), ((5, 300, 70), 1)],
+                         ids=["rows-1000", "rows-16400", "rows-70000", "300x130-dim0", "5x300x70-dim1"])
+def test_softmax_subnormal_tails(dev, ops, orc, dtype, shape, dim):
+    """Lines spanning 110 below their maximum: entries 88-103 below it have
+    subnormal softmax values (float32's, and bfloat16's with the same
+    exponent range), which every kernel must produce rather than 0 -- the
+    bfloat16 bound is one ulp -- and log_softmax's backward takes e^y of
+    them.  Row kernels (register-resident, walked by one block per CU, two
+    reads) and column kernels."""
+    x = np.random.default_rng(31).uniform(-110.0, 0.0, shape).astype(np.float32)
+    a = orc.from_float(x, dtype)
+    d = dev.from_numpy(a, dtype=dtype)
+    k = dim % len(shape)
+    outer, size, inner = int(np.prod(shape[:k])), shape[k], int(np.prod(shape[k + 1:]))
+    g = sample(orc, shape, dtype, 32)
+    for log in (False, True):
+        y = (ops.log_softmax if log else ops.softmax)(d, dim)
+        yh = y.numpy()
+        want = orc.softmax(log, dtype, a, outer, size, inner)
+        if not log:
+            tiny = (as_float(want, dtype) > 0) & (as_float(want, dtype) < 1.17549435e-38)
+            assert tiny.sum() > 0, "the data must produce subnormal softmax values"
+        assert_softmax(yh, want, dtype, log, f"forward log={log}")
+        back = ops._log_softmax_backward_data if log else ops._softmax_backward_data
+        got = back(dev.from_numpy(g, dtype=dtype), y, dim, dtype).numpy()
+        assert_softmax_backward(got, orc.softmax_backward(log, dtype, yh, g, outer, size, inner), dtype, log,
+                                yh, g, outer, size, inner, f"backward log={log}")
+
+
 @pytest.mark.parametrize("D", [1, 7, 64, 256, 1000, 1024, 4096, 4100, 16384, 32000, 65536, 70000])
 def test_softmax_row_lengths(dev, ops, orc, D):
     # every register-resident configuration and the two-read fallback
