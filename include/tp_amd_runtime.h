@@ -65,6 +65,12 @@ int tp_mlu_capture_ready(void);
 /* out[0]: blocks handed out while the last recording ran; out[1]: blocks
  * set aside for recordings (GraphCapture.cpp:65-68). */
 void tp_mlu_capture_stats(int64_t* out);
+/* No counterpart in the reference: how the held recording is replayed.  The
+ * number of kernels tp_mlu_capture_invoke launches one by one (a chain of at
+ * most 16 kernel nodes), or 0 when it launches the HIP graph (longer
+ * recordings, or ones holding copies, events or branches; also when none is
+ * held). */
+int tp_amd_capture_direct_kernels(void);
 
 /* ---- device hooks (MLUHooks.cpp:14-52, MLURuntime.cpp:43-136) ---------- */
 

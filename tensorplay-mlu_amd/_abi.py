@@ -97,6 +97,7 @@ PROTOTYPES = {
     "tp_mlu_capture_reset": (i32, []),
     "tp_mlu_capture_ready": (i32, []),
     "tp_mlu_capture_stats": (None, [I64P]),
+    "tp_amd_capture_direct_kernels": (i32, []),
     "tp_amd_is_available": (i32, []),
     "tp_amd_current_device": (i32, [C.POINTER(C.c_int)]),
     "tp_amd_set_device": (i32, [i32]),

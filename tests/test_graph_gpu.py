@@ -73,6 +73,37 @@ def test_replay_matches_oracle(dev, ops, orc, graph_mod, runtime):
     assert g.stats()[1] == 0
 
 
+@pytest.mark.parametrize("adds", [1, 16, 17, 40])
+def test_short_and_long_recordings(dev, ops, graph_mod, runtime, adds):
+    """A chain of up to 16 kernels is replayed kernel by kernel from the
+    recorded launches, a longer one as the HIP graph: both give the eager
+    result on every refilled input, replayed several times in a row."""
+    rng = np.random.default_rng(adds)
+    x = dev.from_numpy(rng.standard_normal((64, 96)).astype(np.float32))
+    y = dev.from_numpy(rng.standard_normal((64, 96)).astype(np.float32))
+
+    def chain(a, b):
+        for _ in range(adds):
+            a = ops.add(a, b, alpha=0.5)
+        return a
+
+    g = graph_mod.Graph()
+    try:
+        out = g.capture(lambda: chain(x, y))
+        assert graph_mod.Graph.direct_kernels() == (adds if adds <= 16 else 0)
+        for i in range(3):
+            host = rng.standard_normal((64, 96)).astype(np.float32)
+            ops.copy_(x, host)
+            g.replay()
+            g.replay()                              # the same inputs again: the same result
+            runtime.synchronize()
+            want = chain(dev.from_numpy(host), y)
+            assert_bitexact(out.numpy(), want.numpy(), f"{adds} adds, replay {i}")
+    finally:
+        g.reset()
+    assert graph_mod.Graph.direct_kernels() == 0
+
+
 def test_host_read_back_cannot_be_recorded(dev, ops, graph_mod):
     x = dev.from_numpy(np.ones((4, 4), np.float32))
     g = graph_mod.Graph()
