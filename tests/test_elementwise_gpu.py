@@ -217,6 +217,43 @@ def test_activations(dev, ops, orc, dtype):
     assert_bitexact(r.numpy(), orc.unary(8, dtype, a), "relu_")
 
 
+SPECIAL = np.float32([0.0, -0.0, 1.0, -1.0, 1.5, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38, 1e-40,
+                      -1e-40, 1.17549435e-38, 65504.0, 6.1e-5, 5.96e-8, 1e30, 0.5, 2.0, 3.0])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_special_values_bitexact(dev, ops, orc, dtype):
+    """Every pair of special operands -- signed zeros, infinities, NaN,
+    float32 subnormals, the largest float32 and float16 values, the
+    smallest float16 normal and subnormal, as stored in the dtype -- through
+    the arithmetic, scalar, sign and threshold ops: the same bits as the
+    oracle, with a NaN anywhere the oracle has one and the sign of every
+    zero kept."""
+    with np.errstate(over="ignore"):
+        v = orc.from_float(SPECIAL, dtype)
+    a, b = np.repeat(v, len(v)), np.tile(v, len(v))
+    da, db = up(dev, a, dtype), up(dev, b, dtype)
+    cases = [("add", ops.add(da, db), orc.binary(ADD, dtype, a, b, 1.0)),
+             ("sub", ops.sub(da, db), orc.binary(ADD, dtype, a, b, -1.0)),
+             ("add alpha=2", ops.add(da, db, alpha=2), orc.binary(ADD, dtype, a, b, 2.0)),
+             ("mul", ops.mul(da, db), orc.binary(MUL, dtype, a, b)),
+             ("div", ops.div(da, db), orc.binary(DIV, dtype, a, b)),
+             ("mul_scalar 3", ops.mul_scalar(da, 3), orc.affine(dtype, a, 3.0, 0.0)),
+             ("div_scalar 3", ops.div_scalar(da, 3), orc.affine(dtype, a, np.float32(1.0 / 3.0), 0.0)),
+             ("add_scalar 1", ops.add_scalar(da, 1), orc.affine(dtype, a, 1.0, 1.0)),
+             ("neg", ops.neg(da), orc.unary(4, dtype, a)),
+             ("abs", ops.abs(da), orc.unary(5, dtype, a)),
+             ("relu", ops.relu(da), orc.unary(8, dtype, a)),
+             ("square", ops.pow_scalar(da, 2), orc.unary(6, dtype, a)),
+             ("threshold_backward", ops.threshold_backward(db, da, 0), orc.activation_backward(0, dtype, b, a, 0.0))]
+    for what, got, want in cases:
+        g, w = orc.to_float(got.numpy(), dtype), orc.to_float(want, dtype)
+        nan = np.isnan(w)
+        assert np.array_equal(np.isnan(g), nan), f"{what}: NaN in other places"
+        assert np.array_equal(g[~nan], w[~nan]), f"{what}: values differ"
+        assert np.array_equal(np.signbit(g[~nan]), np.signbit(w[~nan])), f"{what}: signs of zero differ"
+
+
 def test_gelu_erf_form_float32_sweep(dev, ops, orc):
     """gelu (erf form) and its backward in float32 over a dense grid of
     [-14, 14] and special values: the rtol 1e-5 bar everywhere, and gelu
