@@ -244,6 +244,80 @@ def test_reductions_of_permuted_views(dev, ops, orc, dtype):
     assert_bitexact(ops.amin(perm, [2]).numpy(), oracle_reduce(orc, AMIN, dtype, bp, [2]), "amin of a permutation")
 
 
+def special_rows():
+    """Rows of 37 normal values with every ordered pair of special values
+    placed in two slots (signed zeros, infinities, NaN, the float32 and
+    float16 extremes, float32 subnormals), and rows made only of NaN, -inf,
+    +inf, -0 or +0."""
+    sp = np.float32([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38, 1e-40, -1e-40,
+                     65504.0, -65504.0, 2.5])
+    rng = np.random.default_rng(0)
+    rows = []
+    for u in sp:
+        for v in sp:
+            r = rng.standard_normal(37).astype(np.float32)
+            r[5], r[17] = u, v
+            rows.append(r)
+    rows += [np.full(37, c, np.float32) for c in (np.nan, -np.inf, np.inf, -0.0, 0.0)]
+    return np.stack(rows)
+
+
+def same_special(got, want, dtype, what, exact, tol=None):
+    """NaN where the oracle has NaN, infinities equal; the rest equal with
+    the sign of zero (exact) or within ``tol`` (per element)."""
+    g, w = as_float(got, dtype).reshape(-1), as_float(want, dtype).reshape(-1)
+    nan = np.isnan(w)
+    assert np.array_equal(np.isnan(g), nan), f"{what}: NaN in other places"
+    inf = np.isinf(w)
+    assert np.array_equal(g[inf], w[inf]), f"{what}: infinities differ"
+    fin = ~nan & ~inf
+    if exact:
+        assert np.array_equal(g[fin], w[fin]) and np.array_equal(np.signbit(g[fin]), np.signbit(w[fin])), what
+    else:
+        bad = np.abs(g[fin] - w[fin]) > tol.reshape(-1)[fin]
+        assert not bad.any(), f"{what}: {int(bad.sum())} beyond the bound"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reductions_and_softmax_special_values(dev, ops, orc, dtype):
+    """Reductions over rows and over columns, and softmax / log_softmax over
+    either axis, of lines holding special values: NaN, infinities and signed
+    zeros as the oracle has them (amax/amin bit-exact), sums within the
+    float32 error of their terms.  A mean whose float32 sum overflows (two
+    3.4e38 terms) is left out: the device sums in float32 and gives +-inf,
+    the oracle in float64 a finite mean."""
+    with np.errstate(over="ignore"):
+        a = orc.from_float(special_rows(), dtype)
+    R, C = a.shape
+    x = as_float(a, dtype).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        exact = x.sum(axis=1)
+        ab = np.nan_to_num(np.abs(x).sum(axis=1), posinf=0.0)
+        over = np.abs(exact) > 3.4028234e38
+    d = dev.from_numpy(a, dtype=dtype)
+    sum_tol = 1e-2 * np.maximum(np.abs(np.nan_to_num(exact, posinf=0, neginf=0)), 1.0) + 4e-6 * ab
+    same_special(ops.sum_dim(d, [1]).numpy(), orc.reduce(SUM, dtype, a, R, C, 1), dtype, "sum rows", False, sum_tol)
+    mean = ops.mean_dim(d, [1]).numpy()
+    want = orc.reduce(MEAN, dtype, a, R, C, 1)
+    same_special(mean[~over], want[~over], dtype, "mean rows", False, sum_tol[~over] / C)
+    for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
+        same_special(fn(d, [1]).numpy(), orc.reduce(op, dtype, a, R, C, 1), dtype, f"op {op} rows", True)
+    at = np.ascontiguousarray(a.T)
+    dt = dev.from_numpy(at, dtype=dtype)
+    same_special(ops.sum_dim(dt, [0]).numpy(), orc.reduce(SUM, dtype, at, 1, C, R), dtype, "sum columns", False,
+                 sum_tol)
+    for op, fn in ((AMAX, ops.amax), (AMIN, ops.amin)):
+        same_special(fn(dt, [0]).numpy(), orc.reduce(op, dtype, at, 1, C, R), dtype, f"op {op} columns", True)
+    for log in (False, True):
+        fn = ops.log_softmax if log else ops.softmax
+        for arr, dd, dim, lines in ((a, d, -1, (R, C, 1)), (at, dt, 0, (1, C, R))):
+            got = fn(dd, dim).numpy()
+            want = orc.softmax(log, dtype, arr, *lines)
+            w = np.abs(as_float(want, dtype).astype(np.float64))
+            tol = (1e-5 * np.maximum(w, 1.0) if log else 1e-5 * w + 1e-30) + (0 if dtype == F32 else 2 * w * 2.0 ** -8)
+            same_special(got, want, dtype, f"softmax log={log} dim={dim}", False, tol)
+
+
 # Shapes for softmax over dim 0 / 1 (inner > 1): one column tile of one
 # slice; several tiles; few tiles over a long D, split into slices whose
 # partials a second launch folds; an odd inner size; enough tiles for one
