@@ -527,3 +527,29 @@ def test_gemm_abi_small_k(amd, dev, orc, dtype, ta, tb, k, cin_kind, bt, m, n):
     got = out.numpy()
     assert not np.isnan(orc.to_float(got, dtype)).any(), "padding leaked into the product"
     check(orc, got, want, dtype, f"small-K gemm {bt}x{m}x{n}x{k} ta={ta} tb={tb} {cin_kind}")
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(64, 64, 64, F32), (512, 512, 512, F32), (512, 512, 512, BF16),
+                                         (4096, 4096, 256, BF16), (1024, 1024, 1024, F32)],
+                         ids=["fma-fp32", "mfma-fp32", "mfma-bf16", "big-bf16", "mfma-fp32-1024"])
+def test_nan_and_inf_propagate(dev, ops, orc, m, n, k, dtype):
+    """NaN and infinities in the operands reach the same entries of C as
+    in IEEE arithmetic: a NaN fills its row (or column), an infinity fills
+    its row except where it meets a 0 (NaN) -- on the FMA kernel, the MFMA
+    kernels and the big bf16 kernel."""
+    rng = np.random.default_rng(k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a[3, 5], a[7, 9], b[9, 11] = np.nan, np.inf, 0.0
+    a[20, :] = 0.0
+    a[20, 30] = -np.inf
+    b[40, 50] = np.nan
+    A, B = orc.from_float(a, dtype), orc.from_float(b, dtype)
+    got = orc.to_float(ops.mm(dev.from_numpy(A, dtype=dtype), dev.from_numpy(B, dtype=dtype)).numpy(), dtype)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = orc.to_float(A, dtype) @ orc.to_float(B, dtype)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), "NaN in other places"
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf), "infinities in other places"
+    assert np.array_equal(got[inf], want[inf]), "signs of the infinities"
+
