@@ -438,3 +438,59 @@ def test_empty_inputs_follow_the_reference(dev, ops, orc):
     dy = sample(orc, (4, 8), F32, 41)
     got = ops.embedding_dense_backward(dev.from_numpy(dy), dev.from_numpy(idx), 3000).numpy()
     assert_bitexact(got, sample_order_sum(orc, F32, dy, idx, 3000, -1, False), "after empty calls")
+
+
+def same_nonfinite(got, want, dtype, what, rel):
+    """NaN and infinities where the oracle has them; the finite rest within
+    ``rel`` of max(|want|, 1)."""
+    g, w = as_float(got, dtype).reshape(-1), as_float(want, dtype).reshape(-1)
+    assert np.array_equal(np.isnan(g), np.isnan(w)), f"{what}: NaN in other places"
+    inf = np.isinf(w)
+    assert np.array_equal(np.isinf(g), inf) and np.array_equal(g[inf], w[inf]), f"{what}: infinities differ"
+    fin = np.isfinite(w)
+    assert np.all(np.abs(g[fin] - w[fin]) <= rel * np.maximum(np.abs(w[fin]), 1.0)), f"{what}: finite values differ"
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_special_values(dev, ops, orc, dtype):
+    """NaN, infinities and constant rows through layer norm and its
+    backward (a NaN or infinite element makes its row NaN, a constant row
+    normalises to the bias), dropout (the mask is the same; a kept NaN stays
+    NaN) and nll_loss (a -inf or NaN target log-probability), against the
+    oracle."""
+    rng = np.random.default_rng(1)
+    D = 256
+    x = rng.standard_normal((8, D)).astype(np.float32)
+    x[1, 3], x[2, 7], x[4, 9] = np.nan, np.inf, -np.inf
+    x[3, :], x[5, :] = 5.0, 0.0
+    X = orc.from_float(x, dtype)
+    w = sample(orc, (D,), dtype, 2)
+    b = sample(orc, (D,), dtype, 3)
+    dX, dw, db = (dev.from_numpy(a, dtype=dtype) for a in (X, w, b))
+    y, mean, rstd = ops.native_layer_norm(dX, (D,), dw, db)
+    wy, wm, wr = orc.layer_norm(dtype, X, D, w, b, 1e-5)
+    tol = 1e-5 if dtype == F32 else 1e-2
+    same_nonfinite(y.numpy(), wy, dtype, "layer norm y", tol)
+    same_nonfinite(mean.numpy(), wm, F32, "layer norm mean", 1e-5)
+    same_nonfinite(rstd.numpy(), wr, F32, "layer norm rstd", 1e-5)
+    dy = sample(orc, (8, D), dtype, 4)
+    gx, gw, gb = ops.native_layer_norm_backward(dev.from_numpy(dy, dtype=dtype), dX, (D,), mean, rstd, dw, db)
+    ox, ow, ob = orc.layer_norm_backward(dtype, dy, X, D, mean.numpy(), rstd.numpy(), w)
+    same_nonfinite(gx.numpy(), ox, dtype, "layer norm dx", 10 * tol)
+    same_nonfinite(gw.numpy(), ow, dtype, "layer norm dweight", 10 * tol)
+    same_nonfinite(gb.numpy(), ob, dtype, "layer norm dbias", 10 * tol)
+    xs = np.tile(np.float32([np.nan, np.inf, -np.inf, -0.0, 0.0, 1.0, -2.0, 3e4]), 4096)
+    XS = orc.from_float(xs, dtype)
+    out, mask = ops.native_dropout(dev.from_numpy(XS, dtype=dtype), 0.3, True, seed=7)
+    wo, wmask = orc.dropout(dtype, XS, 0.3, 7)
+    assert np.array_equal(mask.numpy().astype(np.uint8), wmask), "dropout mask"
+    same_nonfinite(out.numpy(), wo, dtype, "dropout", 0.0)
+    lp = rng.standard_normal((16, 50)).astype(np.float32)
+    lp[2, 4], lp[3, 5], lp[6, 1] = -np.inf, np.nan, np.inf
+    t = np.array([4, 4, 4, 5, 0, 1, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10], np.int64)
+    LP = orc.from_float(lp, dtype)
+    for red in (0, 1, 2):
+        got, _ = ops.nll_loss(dev.from_numpy(LP, dtype=dtype), dev.from_numpy(t), None, red)
+        want, _ = orc.nll_loss(dtype, LP, t, None, red)
+        same_nonfinite(got.numpy(), want, dtype, f"nll_loss reduction {red}", tol)
+
