@@ -102,6 +102,19 @@ __device__ __forceinline__ float phi_fast(float x) {
     return z >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
 }
 
+// Phi(x) and the density phi(x) = e^(-x^2/2) / sqrt(2 pi) together: with
+// z = x / sqrt 2, erfc(|z|) = t e^(-z^2) e^P(t) shares e^(-z^2) with the
+// density (e^P(t) lies in [0.28, 1], so it takes the plain instruction).
+__device__ __forceinline__ float phi_pdf_fast(float x, float& pdf) {
+    const float z = x * kSqrt1_2;
+    const float az = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, az, 1.0f));
+    const float e = exp_fast(-az * az);  // e^(-z^2)
+    const float c = t * e * __builtin_amdgcn_exp2f(erfc_fit(t) * kLog2e);
+    pdf = kInvSqrt2Pi * e;
+    return z >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
+}
+
 // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
 // x * sigmoid(2u), the same function without the cancellation of 1 + tanh(u)
 // for large negative x.
@@ -225,8 +238,7 @@ struct BackwardFn {
         } else if constexpr (OP == TP_AMD_BACKWARD_GELU) {
             float cdf, pdf;
             if constexpr (FAST) {
-                cdf = phi_fast(s);
-                pdf = kInvSqrt2Pi * exp_fast(-0.5f * s * s);
+                cdf = phi_pdf_fast(s, pdf);
             } else {
                 cdf = normal_f32<true>(s, &pdf);
             }
