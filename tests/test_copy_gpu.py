@@ -135,6 +135,27 @@ def test_cast_every_bf16_and_f16_pattern(dev, ops, orc):
         assert_bitexact(got, orc.cast(F32, dtype, f), f"f32 -> {dtype}")
 
 
+def test_cast_every_float32_pattern(dev, ops, orc):
+    """float32 -> float16 and float32 -> bfloat16 at every one of the 2^32
+    float32 bit patterns (16 chunks of 2^28), bit-exact against the oracle's
+    round-to-nearest-even; a NaN stays NaN (its payload is not compared)."""
+    chunk = 1 << 28
+    for c in range((1 << 32) // chunk):
+        bits = (np.arange(chunk, dtype=np.uint64) + np.uint64(c * chunk)).astype(np.uint32)
+        f = bits.view(np.float32)
+        d = dev.from_numpy(f)
+        for dt in (F16, BF16):
+            got, want = ops.to(d, dt).numpy(), orc.cast(F32, dt, f)
+            g, w = got.view(np.uint16), want.view(np.uint16)
+            differ = g != w
+            if differ.any():
+                both_nan = np.isnan(orc.to_float(got, dt)) & np.isnan(orc.to_float(want, dt))
+                bad = np.flatnonzero(differ & ~both_nan)
+                assert bad.size == 0, (f"f32 -> {dt}: {bad.size} patterns differ, first "
+                                       f"{hex(int(bits[bad[0]]))}: got {hex(int(g[bad[0]]))} want {hex(int(w[bad[0]]))}")
+        del d
+
+
 @pytest.mark.parametrize("dtype", ALL)
 def test_fill_and_factories(dev, ops, dtype):
     d = dev.empty((3, 4), dtype)
