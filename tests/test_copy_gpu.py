@@ -128,6 +128,14 @@ def test_cast_every_bf16_and_f16_pattern(dev, ops, orc):
         nan = np.isnan(want)
         assert_bitexact(got[~nan], want[~nan], f"{dtype} -> f32")
         assert np.isnan(got[nan]).all()
+    # 16-bit to 16-bit goes through float32, as the reference's cast table
+    # routes it (CopyKernels.cpp:152-158)
+    for src, dst in ((BF16, F16), (F16, BF16)):
+        got = ops.to(dev.from_numpy(bits, dtype=src), dst).numpy()
+        want = orc.cast(F32, dst, orc.cast(src, F32, bits))
+        nan = np.isnan(orc.to_float(want, dst))
+        assert np.array_equal(np.isnan(orc.to_float(got, dst)), nan), f"{src} -> {dst}: NaN"
+        assert np.array_equal(got.view(np.uint16)[~nan], want.view(np.uint16)[~nan]), f"{src} -> {dst}"
     f = np.random.default_rng(0).standard_normal(1 << 20).astype(np.float32) * 1e3
     f[:6] = [np.inf, -np.inf, 0.0, -0.0, 3.4e38, 1e-40]
     for dtype in (BF16, F16):
