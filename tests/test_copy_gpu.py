@@ -184,6 +184,22 @@ def test_fill_and_factories(dev, ops, dtype):
     assert_bitexact(big.numpy(), np.full((1000, 333), want_val, dtype=NP[dtype]), "large fill")
 
 
+@pytest.mark.parametrize("dtype", [F32, F16, BF16, F64])
+def test_fill_special_values(dev, ops, orc, dtype):
+    """fill_ with -0.0, +-inf, NaN, a float32 subnormal and values that round
+    in the narrow dtypes (0.1, 65519, 1e30): the host encodes the scalar as
+    the reference does (float -> dtype, CopyKernels.cpp:231-291) and every
+    element holds that encoding -- the sign of zero and the NaN included."""
+    d = dev.empty((7, 130), dtype)
+    for value in (-0.0, np.inf, -np.inf, np.nan, 1e-40, 0.1, 65519.0, 1e30):
+        ops.fill_(d, value)
+        got = d.numpy()
+        with np.errstate(over="ignore"):
+            want = np.full(got.shape, orc.from_float(np.float32([value]), dtype)[0]) if dtype != F64 \
+                else np.full(got.shape, np.float64(value))
+        assert np.array_equal(got.view(np.uint8), want.astype(got.dtype).view(np.uint8)), (dtype, value)
+
+
 def test_views_share_device_memory(dev, ops, orc):
     x = values(orc, (4, 6), F32)
     d = dev.from_numpy(x)
