@@ -131,6 +131,58 @@ def test_unary_closed_forms(orc):
     assert np.allclose(g - g[::-1], x, rtol=1e-6)
 
 
+def _round16(v64, dtype, orc):
+    """float64 values -> float32 -> the 16-bit dtype (numpy's float16 rounding
+    and the oracle's bfloat16 rounding, each pinned above), as storage."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        v32 = np.asarray(v64, np.float64).astype(np.float32)
+        return orc.to_bf16(v32) if dtype == BF16 else v32.astype(np.float16)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+def test_transcendentals_at_every_16bit_value(orc, dtype):
+    """Every transcendental unary op and activation derivative of the oracle
+    at every finite 16-bit value, against numpy / scipy float64 rounded the
+    same way (float64 -> float32 -> storage): within one storage ulp, NaN in
+    the same places.  These are the points the GPU's every-value tests
+    compare against."""
+    from scipy import special
+
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    every = bits if dtype == BF16 else bits.view(np.float16)
+    a = every[np.isfinite(orc.to_float(every, dtype))]
+    x = orc.to_float(a, dtype)
+    c = np.sqrt(2.0 / np.pi)
+    with np.errstate(all="ignore"):
+        u = c * (x + 0.044715 * x ** 3)
+        sig = special.expit(x)
+        phi = np.exp(-0.5 * x * x) / np.sqrt(2.0 * np.pi)
+        cdf = 0.5 * special.erfc(-x / np.sqrt(2.0))
+        forward = {0: np.exp(x), 1: np.log(x), 2: np.sqrt(x), 3: 1.0 / np.sqrt(x), 9: sig, 10: np.tanh(x),
+                   11: x * sig, 12: x * cdf, 13: x * special.expit(2.0 * u)}
+        sg = special.expit(2.0 * u)
+        derivative = {3: cdf + x * phi, 5: sig * (1.0 + x * (1.0 - sig)),
+                      4: sg + x * sg * (1.0 - sg) * 2.0 * c * (1.0 + 3.0 * 0.044715 * x * x)}
+    one = np.ones(a.shape, np.float32)
+    ones16 = orc.from_float(one, dtype)
+
+    def check(got, want64, what):
+        want = _round16(want64, dtype, orc)
+        gn, wn = np.isnan(orc.to_float(got, dtype)), np.isnan(orc.to_float(want, dtype))
+        assert np.array_equal(gn, wn), f"{what}: NaN in other places"
+        d = ulp_distance(np.ascontiguousarray(got[~wn]), np.ascontiguousarray(want[~wn]), dtype)
+        assert int(d.max()) <= 1, f"{what}: {int(d.max())} ulp apart"
+
+    for op, want in forward.items():
+        check(orc.unary(op, dtype, a), want, f"unary {op}")
+    for op, want in derivative.items():
+        check(orc.activation_backward(op, dtype, ones16, a), want, f"backward {op}")
+    # sigmoid / tanh backward take the saved output y
+    for op, fwd, f in ((1, 9, lambda y: y * (1.0 - y)), (2, 10, lambda y: 1.0 - y * y)):
+        y = orc.unary(fwd, dtype, a)
+        check(orc.activation_backward(op, dtype, ones16, y), f(orc.to_float(y, dtype)), f"backward {op}")
+
+
 # ---- activation backward (orc_activation_backward) ---------------------------------
 
 @pytest.mark.parametrize("name,op,saved", [("sigmoid", 1, "sigmoid_out"), ("tanh", 2, "tanh_out"),
