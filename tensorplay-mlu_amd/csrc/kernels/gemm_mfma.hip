@@ -1274,6 +1274,7 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 }  // namespace
 
 void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream) {
+    if (launch_gemm_thin(dtype, p, stream)) return;
     switch (dtype) {
         case TP_AMD_FLOAT32: launch_typed<float>(p, stream); break;
         case TP_AMD_BFLOAT16: launch_typed<bf16_t>(p, stream); break;

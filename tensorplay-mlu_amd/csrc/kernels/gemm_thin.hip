@@ -1,0 +1,599 @@
+// Thin products on the matrix cores (gfx950): C = alpha A B + beta Cin
+// where one side of C is at most 32 long -- a decode step's x W^T, a
+// matrix-vector product, the dX = dY W of an LM head, attention over one
+// query.  Such a product reads its large operand once and does almost no
+// arithmetic per byte, so it is bound by HBM; the tiled kernels
+// (gemm_mfma.hip) give it a handful of 64- or 128-wide tiles that each walk
+// all of K on one CU and reach a fifth of the bandwidth.
+//
+// Normal form.  The host turns every eligible product into
+//   C'[i][j] = sum_k X[i][k] W[k][j],  i < m <= 32 ("thin" rows),
+// X the small operand (any strides), W the wide one, stored K-major
+// (element (k, j) at w + j ld + k: a Linear weight, or A of a product with
+// few columns) or N-major (at w + k ld + j: a [K, N] row-major matrix).
+// A product with few columns is taken as its transpose, C^T = B^T A^T, and
+// stores C' transposed (the output strides are free).
+//
+// Work split (stream-K).  A column tile of W (64 or 128 columns) over a
+// step of K (32 of K for 16-bit types) is one unit; the grid has exactly as
+// many 4-wave blocks as fit on the GPU at once, and block b takes units
+// [b U / P, (b + 1) U / P) of the U units in tile-major order, so every
+// block streams the same number of bytes however the shape divides.  Within
+// a block's piece of a tile the four waves take consecutive runs of steps,
+// each with 16 x 16 MFMAs (the thin rows padded with zeros to 16 or 32),
+// two batches of loads in flight; the waves' sums are added in LDS in a
+// fixed tree.  A tile that one block covers whole is written at once.  A
+// tile split between blocks gets a float32 partial from each, stored
+// write-through; the last block to arrive (an arrival counter per tile)
+// adds the partials in block order and writes the tile, so the bits do not
+// depend on timing.
+//
+// Fragments (lane l, c = l % 16, g = l / 16; MFMA output lane l holds rows
+// 4g..4g+3 of column c):
+//   * 16-bit, W K-major: v_mfma_f32_16x16x32; lane l loads W column
+//     (tile column 16 cb + c), k = k0 + 8g .. +7, one 16-byte packet, and the
+//     same k of X row c: the fragment needs no rearranging.
+//   * 16-bit, W N-major: a lane loads 8 consecutive columns 8c .. 8c+7 at the
+//     8 rows k0 + 8g + i and transposes the 8 x 8 block in registers; MFMA j
+//     then multiplies tile columns 8c + j (c = 0..15).
+//   * float32, W K-major: v_mfma_f32_16x16x4_f32; a 16-byte packet gives a
+//     lane k = k0 + 4g .. +3 of one column, fed to 4 MFMAs (MFMA e takes
+//     k0 + 4g + e from X and W alike).
+//   * float32, W N-major: a lane loads 4 consecutive columns 4c .. 4c+3 of
+//     row k0 + g; MFMA j multiplies tile columns 4c + j.
+// The sum pairs X and W elements of the same k in every case, whatever
+// order the matrix core adds them in.
+
+#include <algorithm>
+
+#include "device_common.h"
+#include "gemm.h"
+#include "../allocator.h"
+#include "../common.h"
+#include "../runtime.h"
+#include "tp_amd_kernels.h"
+
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the thin-product fold relies on gfx950's write-through ordering"
+#endif
+
+namespace tp_amd {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThinWaves = 4;
+constexpr int kThinThreads = kThinWaves * kWave;
+constexpr int64_t kThinMaxRows = 32;
+// One arrival counter per tile split between blocks, indexed by the first
+// block that covers the tile (unique among split tiles), each on a 128-byte
+// line of its own: atomics on one line serialize.
+constexpr int kCounterStride = 32;
+constexpr int kMaxThinBlocks = 4096;
+__device__ unsigned int thin_counters[kMaxThinBlocks * kCounterStride];
+
+struct ThinArgs {
+    int64_t m, n, k;    // thin rows (<= 32), columns, depth
+    int64_t tiles;      // column tiles of one batch entry
+    int64_t steps;      // K steps of a tile
+    int64_t units;      // batch * tiles * steps
+    float alpha, beta;
+    const void* x;      // X[i][k] at x + i x_m + k x_k (+ batch x_b)
+    int64_t x_m, x_k, x_b;
+    const void* w;      // W[k][j] at w + j ld + k (K-major) or w + k ld + j
+    int64_t w_ld, w_b;
+    const void* cin;    // read when beta != 0
+    int64_t cin_m, cin_n, cin_b;
+    void* c;            // C'[i][j] at c + i c_m + j c_n (+ batch c_b)
+    int64_t c_m, c_n, c_b;
+    float* part;        // [grid][2][m][TN] float32 partial tiles
+};
+
+template <typename T, bool KMAJOR>
+struct Thin {
+    using S = typename Elem<T>::storage;
+    static constexpr bool k16 = sizeof(S) == 2;
+    static constexpr int V = 16 / sizeof(S);                          // elements per packet
+    static constexpr int STEP = k16 ? 32 : (KMAJOR ? 16 : 4);         // K per step
+    static constexpr int NB = KMAJOR ? 4 : (k16 ? 8 : 4);             // MFMA column groups
+    static constexpr int TN = KMAJOR ? 16 * NB : 16 * NB;             // tile columns
+    static constexpr int WL = KMAJOR ? NB : (k16 ? 8 : 1);            // W packets a step
+    static constexpr int U = k16 ? (KMAJOR ? 2 : 1) : (KMAJOR ? 2 : 8);  // steps a batch
+    // X fragment of a step: 8 (16-bit) or 4 (float32 K-major) consecutive k
+    // as one packet, or one float.
+    static constexpr bool kXPacket = k16 || KMAJOR;
+};
+
+template <typename T, bool KMAJOR, int R>
+struct StepData {
+    uint4 w[Thin<T, KMAJOR>::WL];
+    typename std::conditional<Thin<T, KMAJOR>::kXPacket, uint4, float>::type x[R];
+};
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 mma16(const uint4& a, const uint4& b, f32x4 c) {
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        bf16x8 av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, c, 0, 0, 0);
+    } else {
+        f16x8 av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c, 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Loads go through buffer resources: an offset at or past the resource's
+// size reads zeros, so lanes outside the product (rows past m, columns past
+// n, k past K or past the wave's run) load zeros without a branch, and the
+// loop stays straight-line code whose wait counts the compiler keeps exact.
+// Every valid offset is below 2^31 (checked on the host); kOob plus any
+// offset added to it stays below 2^32.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// A wave's view of one piece of a tile: its resources and per-lane offsets.
+template <typename T, bool KMAJOR, int R, bool XVEC>
+struct ThinWave {
+    using P = Thin<T, KMAJOR>;
+    using S = typename Elem<T>::storage;
+    static constexpr int ES = sizeof(S);
+    __amdgpu_buffer_rsrc_t wres, xres;
+    uint32_t wlane[KMAJOR ? P::NB : 1];  // byte offset of the lane's W column(s), kOob outside the tile
+    uint32_t xlane[R];                   // byte offset of the lane's X rows, kOob past m
+    uint32_t wrow, xk;                   // N-major W bytes per row; X bytes per k
+    int64_t k0, kend;                    // first k of the run; k past the run (and past K)
+    int c, g;
+
+    __device__ __forceinline__ void init(const ThinArgs& p, int64_t bi, int64_t col0, int64_t s_begin,
+                                         int64_t s_end, int lane) {
+        c = lane & 15;
+        g = lane >> 4;
+        k0 = s_begin * P::STEP;
+        kend = s_end * P::STEP < p.k ? s_end * P::STEP : p.k;
+        const int64_t ncols = p.n - col0 < P::TN ? p.n - col0 : P::TN;
+        const S* W = static_cast<const S*>(p.w) + bi * p.w_b;
+        if constexpr (KMAJOR) {
+            wres = make_rsrc(W + col0 * p.w_ld, ((ncols - 1) * p.w_ld + p.k) * ES);
+#pragma unroll
+            for (int cb = 0; cb < P::NB; ++cb) {
+                const int col = 16 * cb + c;
+                wlane[cb] = col < ncols ? static_cast<uint32_t>(col * p.w_ld * ES) : kOob;
+            }
+        } else {
+            // The resource covers rows k0 .. kend - 1: rows past the run read
+            // zeros.
+            const int64_t rows = kend - k0;
+            wres = make_rsrc(W + k0 * p.w_ld + col0, rows > 0 ? ((rows - 1) * p.w_ld + ncols) * ES : 0);
+            const int col = (P::k16 ? 8 : 4) * c;
+            wlane[0] = col < ncols ? static_cast<uint32_t>(col * ES) : kOob;
+            wrow = static_cast<uint32_t>(p.w_ld * ES);
+        }
+        const S* X = static_cast<const S*>(p.x) + bi * p.x_b;
+        xres = make_rsrc(X, ((p.m - 1) * p.x_m + (p.k - 1) * p.x_k + 1) * ES);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = 16 * r + c;
+            xlane[r] = row < p.m ? static_cast<uint32_t>(row * p.x_m * ES) : kOob;
+        }
+        xk = static_cast<uint32_t>(p.x_k * ES);
+    }
+
+    // The loads of step s.
+    __device__ __forceinline__ void load(StepData<T, KMAJOR, R>& d, int64_t s) const {
+        constexpr int V = P::V;
+        if constexpr (P::kXPacket) {
+            const int64_t kv = s * P::STEP + V * g;  // this lane's first k
+            const bool ok = kv < kend;                // K is a whole number of packets where it matters
+            const uint32_t kb = static_cast<uint32_t>(kv * ES);
+            if constexpr (KMAJOR) {
+#pragma unroll
+                for (int cb = 0; cb < P::NB; ++cb) d.w[cb] = load16(wres, ok ? wlane[cb] + kb : kOob);
+            } else {
+                const uint32_t base = wlane[0] + static_cast<uint32_t>(kv - k0) * wrow;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d.w[i] = load16(wres, base + i * wrow);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if constexpr (XVEC) {
+                    d.x[r] = load16(xres, ok ? xlane[r] + kb : kOob);
+                } else {
+                    S e[V];
+#pragma unroll
+                    for (int i = 0; i < V; ++i) {
+                        const uint32_t off = kv + i < kend ? xlane[r] + static_cast<uint32_t>(kv + i) * xk : kOob;
+                        if constexpr (ES == 2) {
+                            e[i] = __builtin_amdgcn_raw_buffer_load_b16(xres, static_cast<int>(off), 0, 0);
+                        } else {
+                            e[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xres, static_cast<int>(off), 0, 0));
+                        }
+                    }
+                    __builtin_memcpy(&d.x[r], e, 16);
+                }
+            }
+        } else {
+            // float32, W N-major: row k0 + g of the step, 4 columns a lane.
+            const int64_t kv = s * P::STEP + g;
+            d.w[0] = load16(wres, wlane[0] + static_cast<uint32_t>(kv - k0) * wrow);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t off = kv < kend ? xlane[r] + static_cast<uint32_t>(kv) * xk : kOob;
+                d.x[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xres, static_cast<int>(off), 0, 0));
+            }
+        }
+    }
+};
+
+template <typename T, bool KMAJOR, int R>
+__device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d, f32x4 (&acc)[R][Thin<T, KMAJOR>::NB]) {
+    using P = Thin<T, KMAJOR>;
+    if constexpr (P::k16) {
+        if constexpr (KMAJOR) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int cb = 0; cb < P::NB; ++cb) acc[r][cb] = mma16<T>(d.x[r], d.w[cb], acc[r][cb]);
+        } else {
+            // 8 rows (k) x 8 columns -> column j's 8 consecutive k.
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                uint32_t f[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t lo = word(d.w[2 * q], j / 2), hi = word(d.w[2 * q + 1], j / 2);
+                    f[q] = (j & 1) ? (lo >> 16) | (hi & 0xffff0000u) : (lo & 0xffffu) | (hi << 16);
+                }
+                const uint4 b = make_uint4(f[0], f[1], f[2], f[3]);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][j] = mma16<T>(d.x[r], b, acc[r][j]);
+            }
+        }
+    } else if constexpr (KMAJOR) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int cb = 0; cb < P::NB; ++cb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[r][cb] = mma32(__uint_as_float(word(d.x[r], e)), __uint_as_float(word(d.w[cb], e)),
+                                       acc[r][cb]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[r][j] = mma32(d.x[r], __uint_as_float(word(d.w[0], j)), acc[r][j]);
+    }
+}
+
+// Steps [s, end) of one tile into acc: batches of U steps, the next batch's
+// loads issued before the current one's MFMAs (steps past `end` load zeros).
+template <typename T, bool KMAJOR, int R, bool XVEC>
+__device__ __forceinline__ void run_steps(const ThinWave<T, KMAJOR, R, XVEC>& wv, int64_t s, int64_t end,
+                                          f32x4 (&acc)[R][Thin<T, KMAJOR>::NB]) {
+    constexpr int U = Thin<T, KMAJOR>::U;
+    if (s >= end) return;
+    StepData<T, KMAJOR, R> a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) wv.load(a[u], s + u);
+    for (;;) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv.load(b[u], s + U + u);
+#pragma unroll
+        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R>(a[u], acc);
+        s += U;
+        if (s >= end) break;
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv.load(a[u], s + U + u);
+#pragma unroll
+        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R>(b[u], acc);
+        s += U;
+        if (s >= end) break;
+    }
+}
+
+// Block holding unit u of `units` split over `blocks` blocks: the largest b
+// with b units / blocks <= u.
+__device__ __forceinline__ int64_t block_of(int64_t u, int64_t units, int64_t blocks) {
+    return ((u + 1) * blocks - 1) / units;
+}
+
+template <typename T>
+__device__ __forceinline__ void store_c(const ThinArgs& p, int64_t bi, int64_t i, int64_t j, float v) {
+    using S = typename Elem<T>::storage;
+    const float a = p.alpha * v;
+    float out = a;
+    if (p.beta != 0.0f) {
+        const S* cin = static_cast<const S*>(p.cin);
+        out = fmaf(p.beta, Elem<T>::load(cin[bi * p.cin_b + i * p.cin_m + j * p.cin_n]), a);
+    }
+    static_cast<S*>(p.c)[bi * p.c_b + i * p.c_m + j * p.c_n] = Elem<T>::store(out);
+}
+
+template <typename T, bool KMAJOR, int R, bool XVEC>
+__global__ __launch_bounds__(kThinThreads) void gemm_thin_kernel(ThinArgs p) {
+    using P = Thin<T, KMAJOR>;
+    constexpr int NB = P::NB, TN = P::TN, E = R * NB * 4;
+    constexpr int EPT = (16 * R * TN + kThinThreads - 1) / kThinThreads;  // fold elements a thread
+    __shared__ float red[kThinWaves / 2][E][kWave];
+    __shared__ float tile[16 * R][TN + 1];
+    __shared__ bool last;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int c = lane & 15, g = lane >> 4;
+    const int64_t blocks = gridDim.x;
+    const int64_t u_begin = static_cast<int64_t>(blockIdx.x) * p.units / blocks;
+    const int64_t u_end = (static_cast<int64_t>(blockIdx.x) + 1) * p.units / blocks;
+    for (int64_t u = u_begin; u < u_end;) {
+        const int64_t t = u / p.steps;  // tile, batch-major
+        const int64_t s0 = u - t * p.steps;
+        const int64_t s1 = std::min(p.steps, s0 + (u_end - u));
+        const int64_t bi = t / p.tiles, col0 = (t - bi * p.tiles) * TN;
+        // This wave's run of the block's steps.
+        const int64_t len = s1 - s0, q = (len + kThinWaves - 1) / kThinWaves;
+        const int64_t ws0 = s0 + std::min(len, wave * q), ws1 = s0 + std::min(len, (wave + 1) * q);
+        f32x4 acc[R][NB];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[r][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (ws0 < ws1) {
+            ThinWave<T, KMAJOR, R, XVEC> wv;
+            wv.init(p, bi, col0, ws0, ws1, lane);
+            run_steps<T, KMAJOR, R, XVEC>(wv, ws0, ws1, acc);
+        }
+        // Waves' sums in a fixed tree: (w0 + w2) + (w1 + w3).
+#pragma unroll
+        for (int half = kThinWaves / 2; half >= 1; half /= 2) {
+            if (wave >= half && wave < 2 * half) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) red[wave - half][(r * NB + j) * 4 + i][lane] = acc[r][j][i];
+            }
+            __syncthreads();
+            if (wave < half) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[r][j][i] += red[wave][(r * NB + j) * 4 + i][lane];
+            }
+            __syncthreads();
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = 16 * r + 4 * g + i;
+                        const int col = KMAJOR ? 16 * j + c : NB * c + j;
+                        tile[row][col] = acc[r][j][i];
+                    }
+        }
+        __syncthreads();
+        const int64_t elems = p.m * TN;
+        if (s0 == 0 && s1 == p.steps) {
+            for (int64_t e = tid; e < elems; e += kThinThreads) {
+                const int64_t i = e / TN, jl = e - i * TN;
+                if (col0 + jl < p.n) store_c<T>(p, bi, i, col0 + jl, tile[i][jl]);
+            }
+        } else {
+            // A piece of a tile shared with other blocks: this block's
+            // partial goes to its slot (0 for its first piece, 1 for its last).
+            float* mine = p.part + (static_cast<int64_t>(blockIdx.x) * 2 + (u == u_begin ? 0 : 1)) * elems;
+            for (int64_t e = tid; e < elems; e += kThinThreads) {
+                const int64_t i = e / TN, jl = e - i * TN;
+                __hip_atomic_store(mine + e, tile[i][jl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            // The partial is written through before the block counts its
+            // arrival; the last arrival's agent-scope loads read it there.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            const int64_t first = block_of(t * p.steps, p.units, blocks);
+            const int64_t final_b = block_of((t + 1) * p.steps - 1, p.units, blocks);
+            if (tid == 0) {
+                unsigned int* ctr = &thin_counters[first * kCounterStride];
+                last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       static_cast<unsigned int>(final_b - first);
+                if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (last) {
+                // Partials of blocks first..final_b added in block order; each
+                // thread's elements of four blocks are loaded before any add.
+                const int64_t tile_start = t * p.steps;
+                float v[EPT];
+#pragma unroll
+                for (int q2 = 0; q2 < EPT; ++q2) v[q2] = 0.0f;
+                for (int64_t b0 = first; b0 <= final_b; b0 += 4) {
+                    float h[4][EPT];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const int64_t b = b0 + d;
+                        // Tile t is block b's first piece when b starts inside it.
+                        const int slot = b * p.units / blocks >= tile_start ? 0 : 1;
+                        const float* src = p.part + (b * 2 + slot) * elems;
+#pragma unroll
+                        for (int q2 = 0; q2 < EPT; ++q2) {
+                            const int64_t e = tid + q2 * kThinThreads;
+                            h[d][q2] = b <= final_b && e < elems
+                                           ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0.0f;
+                        }
+                    }
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+#pragma unroll
+                        for (int q2 = 0; q2 < EPT; ++q2)
+                            if (b0 + d <= final_b) v[q2] += h[d][q2];
+                }
+#pragma unroll
+                for (int q2 = 0; q2 < EPT; ++q2) {
+                    const int64_t e = tid + q2 * kThinThreads;
+                    if (e < elems) {
+                        const int64_t i = e / TN, jl = e - i * TN;
+                        if (col0 + jl < p.n) store_c<T>(p, bi, i, col0 + jl, v[q2]);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // tile and red are reused by the next piece
+        u += s1 - s0;
+    }
+}
+
+template <typename T, bool KMAJOR, int R, bool XVEC>
+int blocks_per_cu() {
+    static const int n = [] {
+        int b = 0;
+        TP_AMD_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, reinterpret_cast<const void*>(gemm_thin_kernel<T, KMAJOR, R, XVEC>), kThinThreads, 0));
+        return std::max(b, 1);
+    }();
+    return n;
+}
+
+template <typename T, bool KMAJOR, int R, bool XVEC>
+void launch_kernel(ThinArgs q, int64_t batch, hipStream_t stream) {
+    using P = Thin<T, KMAJOR>;
+    int device = 0;
+    TP_AMD_HIP_CHECK(hipGetDevice(&device));
+    q.tiles = (q.n + P::TN - 1) / P::TN;
+    q.steps = (q.k + P::STEP - 1) / P::STEP;
+    q.units = batch * q.tiles * q.steps;
+    const int64_t slots = static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, XVEC>()) * cu_count(device);
+    const int64_t grid = std::min<int64_t>({q.units, slots, kMaxThinBlocks});
+    Workspace ws;
+    // Partials exist only when some tile is split between blocks.
+    if (q.units % grid != 0 || (q.units / grid) % q.steps != 0) {
+        ws = Workspace(static_cast<size_t>(grid) * 2 * q.m * P::TN * sizeof(float), device);
+        q.part = static_cast<float*>(ws.get());
+    } else {
+        q.part = nullptr;
+    }
+    gemm_thin_kernel<T, KMAJOR, R, XVEC><<<static_cast<unsigned>(grid), kThinThreads, 0, stream>>>(q);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+template <typename T, bool KMAJOR>
+void launch_rows(const ThinArgs& q, bool xvec, int64_t batch, hipStream_t stream) {
+    if (q.m > 16) {
+        xvec ? launch_kernel<T, KMAJOR, 2, true>(q, batch, stream) : launch_kernel<T, KMAJOR, 2, false>(q, batch, stream);
+    } else {
+        xvec ? launch_kernel<T, KMAJOR, 1, true>(q, batch, stream) : launch_kernel<T, KMAJOR, 1, false>(q, batch, stream);
+    }
+}
+
+template <typename T>
+bool launch_typed(const GemmArgs& p, hipStream_t stream) {
+    using S = typename Elem<T>::storage;
+    constexpr int V = 16 / sizeof(S);
+    constexpr int64_t kLimit = int64_t(1) << 31;
+    if (p.k <= 0 || p.m <= 0 || p.n <= 0 || p.batch <= 0 || p.trans_c) return false;
+    const bool thin_m = p.m <= kThinMaxRows, thin_n = p.n <= kThinMaxRows;
+    if (!thin_m && !thin_n) return false;
+    ThinArgs q{};
+    q.k = p.k;
+    q.alpha = p.alpha;
+    q.beta = p.beta;
+    q.cin = p.cin;
+    bool kmajor;
+    if (thin_m && (!thin_n || p.m <= p.n)) {
+        // X = A, W = B.
+        q.m = p.m;
+        q.n = p.n;
+        q.x = p.a;
+        q.x_m = p.trans_a ? 1 : p.lda;
+        q.x_k = p.trans_a ? p.lda : 1;
+        q.x_b = p.stride_a;
+        q.w = p.b;
+        q.w_ld = p.ldb;
+        q.w_b = p.stride_b;
+        kmajor = p.trans_b;
+        q.c_m = p.ldc;
+        q.c_n = 1;
+        q.cin_m = p.cin_rs;
+        q.cin_n = p.cin_cs;
+    } else {
+        // C^T = B^T A^T: X = B^T, W = A^T.
+        q.m = p.n;
+        q.n = p.m;
+        q.x = p.b;
+        q.x_m = p.trans_b ? p.ldb : 1;
+        q.x_k = p.trans_b ? 1 : p.ldb;
+        q.x_b = p.stride_b;
+        q.w = p.a;
+        q.w_ld = p.lda;
+        q.w_b = p.stride_a;
+        kmajor = !p.trans_a;
+        q.c_m = 1;
+        q.c_n = p.ldc;
+        q.cin_m = p.cin_cs;
+        q.cin_n = p.cin_rs;
+    }
+    q.c = p.c;
+    q.c_b = p.stride_c;
+    q.cin_b = p.cin_stride_b;
+    // The wide operand is read in 16-byte packets along its contiguous axis,
+    // its rows apart (no overlap), and every byte offset within a tile's
+    // resource (and the X resource) below 2^31.
+    constexpr int64_t ES = sizeof(S);
+    if (!aligned16(q.w) || q.w_ld % V != 0 || q.w_b % V != 0 || (kmajor ? q.k : q.n) % V != 0) return false;
+    if (kmajor ? (q.w_ld < q.k || (64 * q.w_ld + q.k) * ES >= kLimit)
+               : (q.w_ld < q.n || ((q.k + 64) * q.w_ld + 128) * ES >= kLimit)) {
+        return false;
+    }
+    if (q.x_m < 0 || q.x_k < 0 || ((q.m - 1) * q.x_m + (q.k + 16) * std::max<int64_t>(q.x_k, 1)) * ES >= kLimit) {
+        return false;
+    }
+    const bool xvec = q.x_k == 1 && q.k % V == 0 && aligned16(q.x) && (q.m == 1 || q.x_m % V == 0) &&
+                      (p.batch == 1 || q.x_b % V == 0);
+    if (kmajor) {
+        launch_rows<T, true>(q, xvec, p.batch, stream);
+    } else {
+        // float32 with W N-major reads one X element a step either way.
+        launch_rows<T, false>(q, xvec && sizeof(S) == 2, p.batch, stream);
+    }
+    return true;
+}
+
+}  // namespace
+
+bool launch_gemm_thin(int dtype, const GemmArgs& p, hipStream_t stream) {
+    switch (dtype) {
+        case TP_AMD_FLOAT32: return launch_typed<float>(p, stream);
+        case TP_AMD_BFLOAT16: return launch_typed<bf16_t>(p, stream);
+        case TP_AMD_FLOAT16: return launch_typed<f16_t>(p, stream);
+        default: return false;
+    }
+}
+
+}  // namespace tp_amd

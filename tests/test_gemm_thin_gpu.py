@@ -1,0 +1,168 @@
+"""Thin products (at most 32 rows or 32 columns of C) on the GPU against the
+float64 product of the same stored operands: the decode-step shapes of a
+Linear layer, a matrix-vector product and an LM head, which run on their
+own kernel (stream-K over column tiles, 16 x 16 MFMAs, partials of tiles
+shared between blocks added in block order).
+
+Bars as for every product (north_star): float32 within 2e-3, bfloat16 and
+float16 within 1e-2 as max |got - want| / max |want|.  Operands are stored
+with NaN padding past their logical extent, so a read outside the operand
+shows as NaN.
+"""
+
+import numpy as np
+import pytest
+
+from _check import BF16, F16, F32
+
+pytestmark = pytest.mark.gpu
+
+BAR = {F32: 2e-3, BF16: 1e-2, F16: 1e-2}
+IDS = {F32: "fp32", BF16: "bf16", F16: "fp16"}
+
+
+def _padded(orc, shape, pad, dtype, seed):
+    x = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * np.float32(0.5)
+    store = np.full(shape[:-1] + (shape[-1] + pad,), np.nan, np.float32)
+    store[..., :shape[-1]] = x
+    return orc.from_float(store, dtype)
+
+
+def _run(lib, dev, orc, dtype, bt, m, n, k, ta, tb, *, pad=8, alpha=1.0, beta=0.0, cin_kind="none",
+         shared_b=False, reps=1, seed=0):
+    """C = alpha op(A) op(B) + beta Cin through tp_amd_launch_gemm; returns
+    (outputs of each rep, float64 expectation)."""
+    a = _padded(orc, (bt, k, m) if ta else (bt, m, k), pad, dtype, seed + 1)
+    b = _padded(orc, (1 if shared_b else bt, n, k) if tb else (1 if shared_b else bt, k, n), pad, dtype,
+                seed + 2)
+    lda, ldb = a.shape[-1], b.shape[-1]
+    A = orc.to_float(a, dtype).astype(np.float64)[..., :(m if ta else k)]
+    B = orc.to_float(b, dtype).astype(np.float64)[..., :(k if tb else n)]
+    A = np.swapaxes(A, -1, -2) if ta else A
+    B = np.swapaxes(B, -1, -2) if tb else B
+    want = alpha * np.matmul(A, B)
+    if cin_kind == "none":
+        cin, rs, cs, sb = None, 0, 0, 0
+    elif cin_kind == "bias-row":
+        cin, rs, cs, sb = _padded(orc, (n,), 0, dtype, seed + 3), 0, 1, 0
+        want = want + beta * orc.to_float(cin, dtype)
+    else:
+        cin, rs, cs, sb = _padded(orc, (bt, m, n), 0, dtype, seed + 3), n, 1, m * n
+        want = want + beta * orc.to_float(cin, dtype)
+    da, db = dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)
+    dc = dev.from_numpy(cin, dtype=dtype) if cin is not None else None
+    outs = []
+    for _ in range(reps):
+        out = dev.empty((bt, m, n), dtype=dtype)
+        st = lib.tp_amd_launch_gemm(0, dtype, bt, m, n, k, alpha, da.data_ptr, lda, a.shape[-2] * lda, int(ta),
+                                    db.data_ptr, ldb, 0 if shared_b else b.shape[-2] * ldb, int(tb), beta,
+                                    dc.data_ptr if dc is not None else 0, rs, cs, sb, out.data_ptr, n, m * n)
+        assert st == 0, lib.tp_mlu_last_error()
+        outs.append(out.numpy())
+    return outs, want
+
+
+def _check(orc, got, want, dtype, what):
+    g = orc.to_float(got, dtype)
+    assert not np.isnan(g).any(), f"{what}: NaN padding reached the product"
+    e = float(np.max(np.abs(g - want)) / max(np.max(np.abs(want)), 1e-30))
+    assert e <= BAR[dtype], f"{what}: relative error {e:.3g} > {BAR[dtype]}"
+
+
+# (m, n, k): thin rows, then the same shapes with the thin side as columns.
+# They cover tiles split between blocks (long K), one step per block (short K
+# over many tiles), ragged column tiles, 16 and 32 thin rows and one more
+# (two MFMA row groups), and a K that is not a whole number of steps.
+THIN = [(1, 1000, 4096), (5, 4104, 40), (16, 520, 1000), (17, 264, 256), (32, 8200, 64), (32, 96, 8192),
+        (3, 17, 2056)]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("m,n,k", THIN + [(n, m, k) for (m, n, k) in THIN],
+                         ids=[f"{m}x{n}x{k}" for (m, n, k) in THIN] + [f"{n}x{m}x{k}" for (m, n, k) in THIN])
+def test_thin_layouts(amd, dev, orc, dtype, ta, tb, m, n, k):
+    lib = amd.load()
+    (got,), want = _run(lib, dev, orc, dtype, 1, m, n, k, ta, tb)
+    _check(orc, got[0], want[0], dtype, f"thin {m}x{n}x{k} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)], ids=["NN", "NT", "TT"])
+@pytest.mark.parametrize("cin_kind", ["bias-row", "full"])
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 1024), (24, 136, 4096), (520, 9, 512)])
+def test_thin_epilogue_batched(amd, dev, orc, dtype, ta, tb, cin_kind, m, n, k):
+    """alpha = 0.5 and beta = 2 with a per-column bias or a full Cin, a
+    batch of 3 (its B shared by the batch, stride 0, in the bias case), and
+    two runs giving the same bits (partials added in block order)."""
+    lib = amd.load()
+    shared = cin_kind == "bias-row"
+    outs, want = _run(lib, dev, orc, dtype, 3, m, n, k, ta, tb, alpha=0.5, beta=2.0, cin_kind=cin_kind,
+                      shared_b=shared, reps=2)
+    assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8)), "thin product not deterministic"
+    _check(orc, outs[0], want, dtype, f"thin batched {m}x{n}x{k} {cin_kind}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=lambda d: IDS[d])
+def test_thin_vector_forms(dev, ops, orc, dtype):
+    """matmul of a vector by a matrix and of a matrix by a vector, linear of
+    one row, addmm with one row and a bias (the ops that reach thin
+    products), against float64."""
+    g = np.random.default_rng(5)
+    mk = lambda *s: orc.from_float(g.standard_normal(s).astype(np.float32), dtype)  # noqa: E731
+    d = lambda x: dev.from_numpy(x, dtype=dtype)  # noqa: E731
+    f = lambda x: orc.to_float(x, dtype).astype(np.float64)  # noqa: E731
+    v, w, x = mk(1536), mk(1536, 2048), mk(2048, 1536)
+    _check(orc, ops.matmul(d(v), d(w)).numpy(), f(v) @ f(w), dtype, "vector @ matrix")
+    _check(orc, ops.matmul(d(x), d(v)).numpy(), f(x) @ f(v), dtype, "matrix @ vector")
+    xr, wl, bias = mk(1, 1536), mk(3000, 1536), mk(3000)
+    _check(orc, ops.linear(d(xr), d(wl), d(bias)).numpy(), f(xr) @ f(wl).T + f(bias), dtype, "linear one row")
+    got = ops.addmm(d(bias), d(xr), d(wl).t(), beta=0.5, alpha=2.0).numpy()
+    _check(orc, got, 0.5 * f(bias) + 2.0 * (f(xr) @ f(wl).T), dtype, "addmm one row")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
+def test_thin_decode_shapes(dev, ops, orc, dtype):
+    """The decode step of config 4's Linear (x [1, 4096] W [11008, 4096]^T),
+    an LM head's logits (x [4, 4096] W [50257, 4096]^T) and its dX
+    (dY [1, 50257] W [50257, 4096], an odd K)."""
+    g = np.random.default_rng(7)
+    mk = lambda *s: orc.from_float(g.standard_normal(s).astype(np.float32), dtype)  # noqa: E731
+    d = lambda x: dev.from_numpy(x, dtype=dtype)  # noqa: E731
+    f = lambda x: orc.to_float(x, dtype).astype(np.float64)  # noqa: E731
+    x, w = mk(1, 4096), mk(11008, 4096)
+    _check(orc, ops.linear(d(x), d(w)).numpy(), f(x) @ f(w).T, dtype, "decode linear")
+    del w
+    head = mk(50257, 4096)
+    dh = d(head)
+    x4 = mk(4, 4096)
+    _check(orc, ops.linear(d(x4), dh).numpy(), f(x4) @ f(head).T, dtype, "LM head logits")
+    dy = mk(1, 50257)
+    _check(orc, ops.mm(d(dy), dh).numpy(), f(dy) @ f(head), dtype, "LM head dX")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("tb", [False, True], ids=["W-N-major", "W-K-major"])
+def test_thin_nan_and_inf(dev, ops, orc, dtype, tb):
+    """A NaN or infinity in one thin row or one wide column reaches exactly
+    the entries IEEE arithmetic gives it, and no others (padding lanes
+    multiply zeros)."""
+    m, n, k = 7, 200, 96
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a[2, 5], a[4, 9] = np.nan, np.inf
+    b[9, 11] = 0.0
+    b[40, 50] = -np.inf
+    A, B = orc.from_float(a, dtype), orc.from_float(b, dtype)
+    dA, dB = dev.from_numpy(A, dtype=dtype), dev.from_numpy(B, dtype=dtype)
+    if tb:
+        dB = dev.from_numpy(np.ascontiguousarray(B.T), dtype=dtype).t()
+    got = orc.to_float(ops.mm(dA, dB).numpy(), dtype)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = orc.to_float(A, dtype).astype(np.float64) @ orc.to_float(B, dtype).astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), "NaN in other places"
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf), "infinities in other places"
+    assert np.array_equal(got[inf], want[inf]), "signs of the infinities"
