@@ -73,6 +73,11 @@ constexpr int64_t kThinMaxRows = 32;
 // line of its own: atomics on one line serialize.
 constexpr int kCounterStride = 32;
 constexpr int kMaxThinBlocks = 4096;
+constexpr int64_t kMinUnits = 4 * kThinWaves;
+// Least bytes of the wide operand for which a product takes this kernel:
+// up to 16 thin rows, and 17 to 32.
+constexpr int64_t kMinWideBytes1 = int64_t(256) << 10;
+constexpr int64_t kMinWideBytes2 = int64_t(8) << 20;
 __device__ unsigned int thin_counters[kMaxThinBlocks * kCounterStride];
 
 struct ThinArgs {
@@ -489,8 +494,14 @@ void launch_kernel(ThinArgs q, int64_t batch, hipStream_t stream) {
     q.tiles = (q.n + P::TN - 1) / P::TN;
     q.steps = (q.k + P::STEP - 1) / P::STEP;
     q.units = batch * q.tiles * q.steps;
-    const int64_t slots = static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, XVEC>()) * cu_count(device);
-    const int64_t grid = std::min<int64_t>({q.units, slots, kMaxThinBlocks});
+    // As many blocks as fit at once.  With fewer tiles than that, tiles are
+    // split, but into pieces of at least kMinUnits steps: a tile split into
+    // many small pieces pays for their fold (a write-through, an atomic and
+    // the reads, each a trip to the coherent level) more than they gain.
+    const int64_t slots = std::min<int64_t>(
+        static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, XVEC>()) * cu_count(device), kMaxThinBlocks);
+    const int64_t tiles = batch * q.tiles;
+    const int64_t grid = std::min<int64_t>(slots, std::max<int64_t>(tiles, q.units / kMinUnits));
     Workspace ws;
     // Partials exist only when some tile is split between blocks.
     if (q.units % grid != 0 || (q.units / grid) % q.steps != 0) {
@@ -574,6 +585,13 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
     if (q.x_m < 0 || q.x_k < 0 || ((q.m - 1) * q.x_m + (q.k + 16) * std::max<int64_t>(q.x_k, 1)) * ES >= kLimit) {
         return false;
     }
+    // Small products stay on the tiled kernels: below these sizes of the wide
+    // operand the thin kernel's fixed costs (resources, the LDS tree, a fold)
+    // outweigh what it saves (measured: bf16 32 x 2048 x 256 6.4 us tiled,
+    // 10.5 us thin; float32 32 x 1024 x 1024 15.9 us tiled, 18.0 us thin;
+    // bf16 1 x 1024 x 1024 12.3 us tiled, 7.9 us thin).
+    const int64_t wbytes = (q.w_b == 0 ? 1 : p.batch) * q.n * q.k * ES;
+    if (wbytes < (q.m > 16 ? kMinWideBytes2 : kMinWideBytes1)) return false;
     const bool xvec = q.x_k == 1 && q.k % V == 0 && aligned16(q.x) && (q.m == 1 || q.x_m % V == 0) &&
                       (p.batch == 1 || q.x_b % V == 0);
     if (kmajor) {
