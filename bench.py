@@ -19,8 +19,9 @@ Also reported on the same line:
   cold: four inputs and four outputs rotated, 2 GiB, beyond the 256 MB
   Infinity Cache; ``roofline_warm`` is the same kernel on one input and
   output reused every launch;
-* ``suite``: per-kernel throughput of configs 2-5 and of the neural-network
-  layers (GB/s or TFLOP/s and the fraction of the matching MI355X peak), each
+* ``suite``: per-kernel throughput of configs 2-5, of thin (decode-step)
+  products and of the neural-network layers (GB/s or TFLOP/s and the
+  fraction of the matching MI355X peak), each
   from HIP events, and the reference README's benchmark rows beside the
   MLU590 times it publishes (``readme_rows``);
 * ``cpu_baseline``: the repository's C oracle (a CPU port of the same
@@ -31,7 +32,7 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,bmm,reduce,reduce_all,softmax,nn,mlp,odd}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,bmm,reduce,reduce_all,softmax,nn,mlp,odd,thin}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -301,6 +302,58 @@ def suite_gemm(ops, dev, ev):
     a, b = put((64, 512, 128), BF16, 128 ** -0.25), put((64, 128, 512), BF16, 128 ** -0.25)
     record("bmm_64x512x128x512", lambda: ops.bmm(a, b), 2 * 64 * 512 * 512 * 128, BF16,
            nbytes=(64 * 512 * 128 * 2 + 64 * 512 * 512) * 2)
+    return out
+
+
+def thin_cases(ops, dev):
+    """Thin products of a decode step, each with its wide operand in several
+    copies (rotated, so that the copies together exceed the 256 MB Infinity
+    Cache): (name, launch, bytes moved a launch, copies)."""
+    g = np.random.default_rng(0)
+
+    def put(shape, dtype, scale=1.0):
+        d = dev.from_numpy(g.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+        return d if dtype == F32 else ops.to(d, dtype)
+
+    def copies(w, n):
+        return [w] + [ops.add_scalar(w, 0.001 * k) for k in range(1, n)]
+
+    cases = []
+    for dtype in (BF16, F32):
+        e = ESIZE[dtype]
+        w = copies(put((11008, 4096), dtype, 4096 ** -0.5), 4)
+        for m in (1, 16):
+            x = put((m, 4096), dtype)
+            cases.append((f"linear_{m}x4096x11008_{NAME[dtype]}", x, w, lambda x, w: ops.linear(x, w),
+                          (11008 * 4096 + m * 4096 + m * 11008) * e))
+        del w
+    head = copies(put((50257, 4096), BF16, 4096 ** -0.5), 2)
+    x = put((1, 4096), BF16)
+    cases.append(("lm_head_logits_1x4096x50257_bf16", x, head, lambda x, w: ops.linear(x, w),
+                  (50257 * 4096 + 4096 + 50257) * 2))
+    dy = put((1, 50257), BF16)
+    cases.append(("lm_head_dx_1x50257x4096_bf16", dy, head, lambda x, w: ops.mm(x, w),
+                  (50257 * 4096 + 50257 + 4096) * 2))
+    return cases
+
+
+def suite_thin(ops, dev, ev):
+    """Thin products (decode-step shapes): GB/s against HBM, the wide
+    operand rotated over copies beyond the Infinity Cache."""
+    out = {}
+    for name, x, ws, fn, nbytes in thin_cases(ops, dev):
+        k = [0]
+
+        def call(x=x, ws=ws, fn=fn):
+            fn(x, ws[k[0] % len(ws)])
+            k[0] += 1
+        for _ in range(len(ws)):
+            call()
+        reps = 10 * len(ws)
+        ms = ev.time_ms(call, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                     "copies": len(ws)}
     return out
 
 
@@ -904,11 +957,19 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              dropout p = 0.1 and its backward, embedding of 8192 indices into
              [32000, 4096] and its dense gradient, nll_loss over
              [8192, 32000] and its backward;
+    thin:    the thin products of the suite (decode-step Linear layers,
+             an LM head's logits and dX), ten launches each, the wide
+             operand rotated over its copies;
     odd:     products whose operands the matrix cores cannot read in place,
              repacked: ten bf16 mm 2047^3 and five bf16 [2048, 4096] x
              [4096, 50257]; then binary ops with transposed inputs, fp32 and
              bf16 4096^2, ten x.t() + y and ten x.t() * y.t() each."""
     import ctypes as C
+    if what == "thin":
+        for name, x, ws, fn, _ in thin_cases(ops, dev):
+            for k in range(10):
+                fn(x, ws[k % len(ws)])
+        return
     if what == "traffic_cold":
         a = dev.from_numpy(np.full((N, N), 1.5, np.float32))
         row = dev.from_numpy(np.full((N,), 0.5, np.float32))
@@ -1106,7 +1167,7 @@ def main() -> int:
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "vs_torch", "bmm",
-                                         "reduce", "reduce_all", "softmax", "nn", "mlp", "odd"],
+                                         "reduce", "reduce_all", "softmax", "nn", "mlp", "odd", "thin"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
@@ -1192,6 +1253,7 @@ def main() -> int:
         del tensors
         suite["config3"] = section("config 3", lambda: suite_config3(ops, dev, ev))
         suite["config4_5a"] = section("configs 4 and 5a", lambda: suite_gemm(ops, dev, ev))
+        suite["thin"] = section("thin products", lambda: suite_thin(ops, dev, ev))
         suite["config5b"] = section("config 5b", lambda: suite_config5b(ops, dev, ev))
         suite["nn"] = section("NN layers", lambda: suite_nn(ops, dev, ev))
         suite["readme_rows"] = section("the reference README's rows", lambda: suite_readme(ops, dev, ev, lib))

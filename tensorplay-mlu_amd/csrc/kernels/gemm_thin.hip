@@ -73,10 +73,10 @@ constexpr int64_t kThinMaxRows = 32;
 // line of its own: atomics on one line serialize.
 constexpr int kCounterStride = 32;
 constexpr int kMaxThinBlocks = 4096;
-constexpr int64_t kMinUnits = 4 * kThinWaves;
+constexpr int64_t kMinPieceBytes = int64_t(64) << 10;
 // Least bytes of the wide operand for which a product takes this kernel:
 // up to 16 thin rows, and 17 to 32.
-constexpr int64_t kMinWideBytes1 = int64_t(256) << 10;
+constexpr int64_t kMinWideBytes1 = int64_t(1) << 20;
 constexpr int64_t kMinWideBytes2 = int64_t(8) << 20;
 __device__ unsigned int thin_counters[kMaxThinBlocks * kCounterStride];
 
@@ -97,25 +97,39 @@ struct ThinArgs {
     float* part;        // [grid][2][m][TN] float32 partial tiles
 };
 
-template <typename T, bool KMAJOR>
+template <typename T, bool KMAJOR, int R>
 struct Thin {
     using S = typename Elem<T>::storage;
     static constexpr bool k16 = sizeof(S) == 2;
-    static constexpr int V = 16 / sizeof(S);                          // elements per packet
-    static constexpr int STEP = k16 ? 32 : (KMAJOR ? 16 : 4);         // K per step
-    static constexpr int NB = KMAJOR ? 4 : (k16 ? 8 : 4);             // MFMA column groups
-    static constexpr int TN = KMAJOR ? 16 * NB : 16 * NB;             // tile columns
-    static constexpr int WL = KMAJOR ? NB : (k16 ? 8 : 1);            // W packets a step
-    static constexpr int U = k16 ? (KMAJOR ? 2 : 1) : (KMAJOR ? 2 : 8);  // steps a batch
-    // X fragment of a step: 8 (16-bit) or 4 (float32 K-major) consecutive k
-    // as one packet, or one float.
+    static constexpr int V = 16 / sizeof(S);               // elements per packet
+    static constexpr int NB = KMAJOR ? 4 : (k16 ? 8 : 4);  // MFMA column groups
+    static constexpr int TN = 16 * NB;                     // tile columns
+    // K-major W: a step gives each lane HALVES packets of a column, lane g
+    // taking packets HALVES g .. HALVES g + HALVES - 1 of the step's k, so
+    // one column's packets of a step go out as back-to-back loads that
+    // cover whole 128-byte lines (with one packet a lane, the two halves of
+    // a line were requested a step apart and some lines were fetched twice:
+    // FETCH_SIZE 1.116x the operand for bf16 1 x 4096 x 11008).  float32
+    // with 17-32 rows keeps one packet, for registers.
+    static constexpr int HALVES = KMAJOR && !(!k16 && R == 2) ? 2 : 1;
+    static constexpr int STEP = KMAJOR ? 4 * V * HALVES : (k16 ? 32 : 4);  // K per step
+    static constexpr int WL = KMAJOR ? NB * HALVES : (k16 ? 8 : 1);       // W packets a step
+    static constexpr int XL = KMAJOR ? HALVES : 1;                        // X fragments a row
+    // Steps a batch of loads, and blocks a CU the registers are sized for
+    // (float32 K-major with 17-32 rows: one packet a step at two blocks a
+    // CU, 32 x 11008 x 4096 in 47 us against 58 us at two and one block).
+    static constexpr int U = KMAJOR ? 1 : (k16 ? 1 : 8);
+    static constexpr int OCCUPANCY = (!k16 && KMAJOR && R == 2) ? 2 : 1;
+    // X fragment: 8 (16-bit) or 4 (float32 K-major) consecutive k as one
+    // packet, or one float.
     static constexpr bool kXPacket = k16 || KMAJOR;
 };
 
 template <typename T, bool KMAJOR, int R>
 struct StepData {
-    uint4 w[Thin<T, KMAJOR>::WL];
-    typename std::conditional<Thin<T, KMAJOR>::kXPacket, uint4, float>::type x[R];
+    using P = Thin<T, KMAJOR, R>;
+    uint4 w[P::WL];
+    typename std::conditional<P::kXPacket, uint4, float>::type x[R * P::XL];
 };
 
 __device__ __forceinline__ uint32_t word(const uint4& v, int i) {
@@ -163,7 +177,7 @@ __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // A wave's view of one piece of a tile: its resources and per-lane offsets.
 template <typename T, bool KMAJOR, int R, bool XVEC>
 struct ThinWave {
-    using P = Thin<T, KMAJOR>;
+    using P = Thin<T, KMAJOR, R>;
     using S = typename Elem<T>::storage;
     static constexpr int ES = sizeof(S);
     __amdgpu_buffer_rsrc_t wres, xres;
@@ -209,37 +223,50 @@ struct ThinWave {
 
     // The loads of step s.
     __device__ __forceinline__ void load(StepData<T, KMAJOR, R>& d, int64_t s) const {
-        constexpr int V = P::V;
+        constexpr int V = P::V, H = P::XL;
         if constexpr (P::kXPacket) {
-            const int64_t kv = s * P::STEP + V * g;  // this lane's first k
-            const bool ok = kv < kend;                // K is a whole number of packets where it matters
-            const uint32_t kb = static_cast<uint32_t>(kv * ES);
+            // This lane's packets: k = kv[h] .. kv[h] + V - 1.
+            int64_t kv[H];
+            bool ok[H];
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                kv[h] = s * P::STEP + V * (H * g + h);
+                ok[h] = kv[h] < kend;  // K is a whole number of packets where it matters
+            }
             if constexpr (KMAJOR) {
 #pragma unroll
-                for (int cb = 0; cb < P::NB; ++cb) d.w[cb] = load16(wres, ok ? wlane[cb] + kb : kOob);
+                for (int cb = 0; cb < P::NB; ++cb)
+#pragma unroll
+                    for (int h = 0; h < H; ++h)
+                        d.w[cb * H + h] =
+                            load16(wres, ok[h] ? wlane[cb] + static_cast<uint32_t>(kv[h] * ES) : kOob);
             } else {
-                const uint32_t base = wlane[0] + static_cast<uint32_t>(kv - k0) * wrow;
+                const uint32_t base = wlane[0] + static_cast<uint32_t>(kv[0] - k0) * wrow;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d.w[i] = load16(wres, base + i * wrow);
             }
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if constexpr (XVEC) {
-                    d.x[r] = load16(xres, ok ? xlane[r] + kb : kOob);
-                } else {
-                    S e[V];
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-                    for (int i = 0; i < V; ++i) {
-                        const uint32_t off = kv + i < kend ? xlane[r] + static_cast<uint32_t>(kv + i) * xk : kOob;
-                        if constexpr (ES == 2) {
-                            e[i] = __builtin_amdgcn_raw_buffer_load_b16(xres, static_cast<int>(off), 0, 0);
-                        } else {
-                            e[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xres, static_cast<int>(off), 0, 0));
+                for (int h = 0; h < H; ++h) {
+                    if constexpr (XVEC) {
+                        d.x[r * H + h] = load16(xres, ok[h] ? xlane[r] + static_cast<uint32_t>(kv[h] * ES) : kOob);
+                    } else {
+                        S e[V];
+#pragma unroll
+                        for (int i = 0; i < V; ++i) {
+                            const int64_t k = kv[h] + i;
+                            const uint32_t off = k < kend ? xlane[r] + static_cast<uint32_t>(k) * xk : kOob;
+                            if constexpr (ES == 2) {
+                                e[i] = __builtin_amdgcn_raw_buffer_load_b16(xres, static_cast<int>(off), 0, 0);
+                            } else {
+                                e[i] = __uint_as_float(
+                                    __builtin_amdgcn_raw_buffer_load_b32(xres, static_cast<int>(off), 0, 0));
+                            }
                         }
+                        __builtin_memcpy(&d.x[r * H + h], e, 16);
                     }
-                    __builtin_memcpy(&d.x[r], e, 16);
                 }
-            }
         } else {
             // float32, W N-major: row k0 + g of the step, 4 columns a lane.
             const int64_t kv = s * P::STEP + g;
@@ -254,14 +281,18 @@ struct ThinWave {
 };
 
 template <typename T, bool KMAJOR, int R>
-__device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d, f32x4 (&acc)[R][Thin<T, KMAJOR>::NB]) {
-    using P = Thin<T, KMAJOR>;
+__device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d,
+                                         f32x4 (&acc)[R][Thin<T, KMAJOR, R>::NB]) {
+    using P = Thin<T, KMAJOR, R>;
+    constexpr int H = P::XL;
     if constexpr (P::k16) {
         if constexpr (KMAJOR) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int cb = 0; cb < P::NB; ++cb) acc[r][cb] = mma16<T>(d.x[r], d.w[cb], acc[r][cb]);
+                for (int cb = 0; cb < P::NB; ++cb)
+#pragma unroll
+                    for (int h = 0; h < H; ++h) acc[r][cb] = mma16<T>(d.x[r * H + h], d.w[cb * H + h], acc[r][cb]);
         } else {
             // 8 rows (k) x 8 columns -> column j's 8 consecutive k.
 #pragma unroll
@@ -283,9 +314,11 @@ __device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d, f32x4 
 #pragma unroll
             for (int cb = 0; cb < P::NB; ++cb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[r][cb] = mma32(__uint_as_float(word(d.x[r], e)), __uint_as_float(word(d.w[cb], e)),
-                                       acc[r][cb]);
+                for (int h = 0; h < H; ++h)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[r][cb] = mma32(__uint_as_float(word(d.x[r * H + h], e)),
+                                           __uint_as_float(word(d.w[cb * H + h], e)), acc[r][cb]);
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -298,8 +331,8 @@ __device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d, f32x4 
 // loads issued before the current one's MFMAs (steps past `end` load zeros).
 template <typename T, bool KMAJOR, int R, bool XVEC>
 __device__ __forceinline__ void run_steps(const ThinWave<T, KMAJOR, R, XVEC>& wv, int64_t s, int64_t end,
-                                          f32x4 (&acc)[R][Thin<T, KMAJOR>::NB]) {
-    constexpr int U = Thin<T, KMAJOR>::U;
+                                          f32x4 (&acc)[R][Thin<T, KMAJOR, R>::NB]) {
+    constexpr int U = Thin<T, KMAJOR, R>::U;
     if (s >= end) return;
     StepData<T, KMAJOR, R> a[U], b[U];
 #pragma unroll
@@ -339,8 +372,9 @@ __device__ __forceinline__ void store_c(const ThinArgs& p, int64_t bi, int64_t i
 }
 
 template <typename T, bool KMAJOR, int R, bool XVEC>
-__global__ __launch_bounds__(kThinThreads) void gemm_thin_kernel(ThinArgs p) {
-    using P = Thin<T, KMAJOR>;
+__global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void gemm_thin_kernel(
+    ThinArgs p) {
+    using P = Thin<T, KMAJOR, R>;
     constexpr int NB = P::NB, TN = P::TN, E = R * NB * 4;
     constexpr int EPT = (16 * R * TN + kThinThreads - 1) / kThinThreads;  // fold elements a thread
     __shared__ float red[kThinWaves / 2][E][kWave];
@@ -488,20 +522,21 @@ int blocks_per_cu() {
 
 template <typename T, bool KMAJOR, int R, bool XVEC>
 void launch_kernel(ThinArgs q, int64_t batch, hipStream_t stream) {
-    using P = Thin<T, KMAJOR>;
+    using P = Thin<T, KMAJOR, R>;
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     q.tiles = (q.n + P::TN - 1) / P::TN;
     q.steps = (q.k + P::STEP - 1) / P::STEP;
     q.units = batch * q.tiles * q.steps;
     // As many blocks as fit at once.  With fewer tiles than that, tiles are
-    // split, but into pieces of at least kMinUnits steps: a tile split into
-    // many small pieces pays for their fold (a write-through, an atomic and
-    // the reads, each a trip to the coherent level) more than they gain.
+    // split, but into pieces of at least kMinPieceBytes of W: a tile split
+    // into many small pieces pays for their fold (a write-through, an atomic
+    // and the reads, each a trip to the coherent level) more than they gain.
     const int64_t slots = std::min<int64_t>(
         static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, XVEC>()) * cu_count(device), kMaxThinBlocks);
     const int64_t tiles = batch * q.tiles;
-    const int64_t grid = std::min<int64_t>(slots, std::max<int64_t>(tiles, q.units / kMinUnits));
+    const int64_t min_units = std::max<int64_t>(1, kMinPieceBytes / (P::STEP * P::TN * sizeof(typename Elem<T>::storage)));
+    const int64_t grid = std::min<int64_t>(slots, std::max<int64_t>(tiles, q.units / min_units));
     Workspace ws;
     // Partials exist only when some tile is split between blocks.
     if (q.units % grid != 0 || (q.units / grid) % q.steps != 0) {
@@ -589,7 +624,8 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
     // operand the thin kernel's fixed costs (resources, the LDS tree, a fold)
     // outweigh what it saves (measured: bf16 32 x 2048 x 256 6.4 us tiled,
     // 10.5 us thin; float32 32 x 1024 x 1024 15.9 us tiled, 18.0 us thin;
-    // bf16 1 x 1024 x 1024 12.3 us tiled, 7.9 us thin).
+    // bf16 16 x 512 x 512 7.9 us tiled, 10.1 us thin; bf16 1 x 1024 x 1024
+    // 12.3 us tiled, 7.9 us thin).
     const int64_t wbytes = (q.w_b == 0 ? 1 : p.batch) * q.n * q.k * ES;
     if (wbytes < (q.m > 16 ? kMinWideBytes2 : kMinWideBytes1)) return false;
     const bool xvec = q.x_k == 1 && q.k % V == 0 && aligned16(q.x) && (q.m == 1 || q.x_m % V == 0) &&

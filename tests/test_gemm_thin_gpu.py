@@ -73,11 +73,11 @@ def _check(orc, got, want, dtype, what):
 # They cover tiles split between blocks (long K), one step per block (short K
 # over many tiles), ragged column tiles, 16 and 32 thin rows and one more
 # (two MFMA row groups), and a K that is not a whole number of steps.  The
-# wide operand is at least 256 KiB (8 MiB past 16 thin rows), the sizes
-# from which products take the thin kernel; the last shape is below that
-# and checks the tiled kernels still take it.
-THIN = [(1, 1000, 4096), (5, 4104, 40), (16, 520, 1000), (17, 4104, 1024), (32, 8200, 512), (32, 512, 8200),
-        (3, 72, 2056), (3, 17, 2056)]
+# wide operand is at least 1 MiB (8 MiB past 16 thin rows), the sizes from
+# which products take the thin kernel; the last shape is below that and
+# checks the tiled kernels still take it.
+THIN = [(1, 1000, 4096), (5, 4104, 136), (16, 520, 1024), (17, 4104, 1024), (32, 8200, 512), (32, 512, 8200),
+        (3, 264, 2056), (3, 17, 2056)]
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=lambda d: IDS[d])
@@ -94,7 +94,7 @@ def test_thin_layouts(amd, dev, orc, dtype, ta, tb, m, n, k):
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)], ids=["NN", "NT", "TT"])
 @pytest.mark.parametrize("cin_kind", ["bias-row", "full"])
-@pytest.mark.parametrize("m,n,k", [(1, 1000, 1024), (24, 1040, 4096), (520, 9, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 1024), (24, 1040, 4096), (1032, 9, 512)])
 def test_thin_epilogue_batched(amd, dev, orc, dtype, ta, tb, cin_kind, m, n, k):
     """alpha = 0.5 and beta = 2 with a per-column bias or a full Cin, a
     batch of 3 (its B shared by the batch, stride 0, in the bias case), and
@@ -151,7 +151,7 @@ def test_thin_nan_and_inf(dev, ops, orc, dtype, tb):
     """A NaN or infinity in one thin row or one wide column reaches exactly
     the entries IEEE arithmetic gives it, and no others (padding lanes
     multiply zeros)."""
-    m, n, k = 7, 2000, 96
+    m, n, k = 7, 2000, 264
     rng = np.random.default_rng(3)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
