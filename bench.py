@@ -32,7 +32,8 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,bmm,reduce,reduce_all,softmax,nn,mlp,odd,thin}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,vs_torch_thin,bmm,reduce,
+                             reduce_all,softmax,nn,mlp,odd,thin}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -957,6 +958,10 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              dropout p = 0.1 and its backward, embedding of 8192 indices into
              [32000, 4096] and its dense gradient, nll_loss over
              [8192, 32000] and its backward;
+    vs_torch_thin: thin bf16 products of a decode step (Linear of 1 and
+             16 rows, x @ W with W [4096, 11008], an LM head's logits and
+             dX), this library and torch interleaved as in vs_torch, each
+             rotating over its own copies of the wide operand;
     thin:    the thin products of the suite (decode-step Linear layers,
              an LM head's logits and dX), ten launches each, the wide
              operand rotated over its copies;
@@ -1052,6 +1057,49 @@ def profile_launches(what: str, lib, ops, dev) -> None:
         cases = [(lambda: ops.mm(a, b), lambda: torch.mm(ta, tb)),
                  (lambda: ops.mm(a, b.t()), lambda: torch.mm(ta, tb.t())),
                  (lambda: ops.linear(x, w, bias), lambda: F.linear(tx, tw, tbias))]
+
+        def drain():
+            assert lib.tp_amd_synchronize(0) == 0
+            torch.cuda.synchronize()
+
+        for rnd in range(4):
+            for ours, theirs in cases:
+                for fn in ((ours, theirs) if rnd % 2 == 0 else (theirs, ours)):
+                    for _ in range(10):
+                        fn()
+                    drain()
+    elif what == "vs_torch_thin":
+        # Thin bf16 products of a decode step from this library and from
+        # torch on the same GPU, interleaved as in vs_torch, each library
+        # rotating over its own copies of the wide operand.
+        import torch
+        F = torch.nn.functional
+        g = np.random.default_rng(0)
+
+        def both(shape, copies=1):
+            a32 = g.standard_normal(shape, dtype=np.float32) * np.float32(shape[-1] ** -0.5)
+            ours = ops.to(dev.from_numpy(a32), BF16)
+            theirs = torch.from_numpy(a32).to("cuda").to(torch.bfloat16)
+            del a32
+            return ([ours] + [ops.add_scalar(ours, 0.001 * k) for k in range(1, copies)],
+                    [theirs] + [theirs + 0.001 * k for k in range(1, copies)])
+
+        w, tw = both((11008, 4096), 4)
+        wn, twn = both((4096, 11008), 4)
+        x1, tx1 = both((1, 4096))
+        x16, tx16 = both((16, 4096))
+        head, thead = both((50257, 4096), 2)
+        dy, tdy = both((1, 50257))
+        k = [0]
+
+        def rot(ws):
+            k[0] += 1
+            return ws[k[0] % len(ws)]
+        cases = [(lambda: ops.linear(x1[0], rot(w)), lambda: F.linear(tx1[0], rot(tw))),
+                 (lambda: ops.linear(x16[0], rot(w)), lambda: F.linear(tx16[0], rot(tw))),
+                 (lambda: ops.mm(x1[0], rot(wn)), lambda: torch.mm(tx1[0], rot(twn))),
+                 (lambda: ops.linear(x1[0], rot(head)), lambda: F.linear(tx1[0], rot(thead))),
+                 (lambda: ops.mm(dy[0], rot(head)), lambda: torch.mm(tdy[0], rot(thead)))]
 
         def drain():
             assert lib.tp_amd_synchronize(0) == 0
@@ -1167,7 +1215,8 @@ def main() -> int:
     p.add_argument("--no-suite", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "vs_torch", "bmm",
-                                         "reduce", "reduce_all", "softmax", "nn", "mlp", "odd", "thin"],
+                                         "reduce", "reduce_all", "softmax", "nn", "mlp", "odd", "thin",
+                                         "vs_torch_thin"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
@@ -1175,7 +1224,7 @@ def main() -> int:
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         return 2
 
-    if args.profile == "vs_torch":
+    if args.profile in ("vs_torch", "vs_torch_thin"):
         # torch's GPU path loads its own copy of the HIP runtime by a name
         # this library does not ask for; loaded first, it is the one copy in
         # the process, and this library binds to it by soname.  Loaded after
