@@ -14,14 +14,16 @@
 // A product with few columns is taken as its transpose, C^T = B^T A^T, and
 // stores C' transposed (the output strides are free).
 //
-// Work split (stream-K).  A column tile of W (64 or 128 columns) over a
-// step of K (32 of K for 16-bit types) is one unit; the grid has exactly as
-// many 4-wave blocks as fit on the GPU at once, and block b takes units
-// [b U / P, (b + 1) U / P) of the U units in tile-major order, so every
-// block streams the same number of bytes however the shape divides.  Within
-// a block's piece of a tile the four waves take consecutive runs of steps,
+// Work split.  A column tile of W (64 or 128 columns) over a step of K (64
+// of K for 16-bit types with W K-major) is one unit.  With at least as
+// many tiles as blocks fit on the GPU at once, every block takes whole
+// tiles; the tiles left over (fewer than a round) are first split into
+// equal runs of units over the blocks (stream-K), so that their folds
+// overlap the whole tiles still streaming.  With fewer tiles than that,
+// every tile is split, into pieces of at least 64 KiB of W.  Within a
+// block's piece of a tile the four waves take consecutive runs of steps,
 // each with 16 x 16 MFMAs (the thin rows padded with zeros to 16 or 32),
-// two batches of loads in flight; the waves' sums are added in LDS in a
+// the next batch of loads in flight; the waves' sums are added in LDS in a
 // fixed tree.  A tile that one block covers whole is written at once.  A
 // tile split between blocks gets a float32 partial from each, stored
 // write-through; the last block to arrive (an arrival counter per tile)
@@ -74,6 +76,8 @@ constexpr int64_t kThinMaxRows = 32;
 constexpr int kCounterStride = 32;
 constexpr int kMaxThinBlocks = 4096;
 constexpr int64_t kMinPieceBytes = int64_t(64) << 10;
+constexpr int64_t kMinSplitBytes = int64_t(16) << 10;
+constexpr int64_t kSplitTileBytes = int64_t(256) << 10;
 // Least bytes of the wide operand for which a product takes this kernel:
 // up to 16 thin rows, and 17 to 32.
 constexpr int64_t kMinWideBytes1 = int64_t(1) << 20;
@@ -84,7 +88,6 @@ struct ThinArgs {
     int64_t m, n, k;    // thin rows (<= 32), columns, depth
     int64_t tiles;      // column tiles of one batch entry
     int64_t steps;      // K steps of a tile
-    int64_t units;      // batch * tiles * steps
     float alpha, beta;
     const void* x;      // X[i][k] at x + i x_m + k x_k (+ batch x_b)
     int64_t x_m, x_k, x_b;
@@ -94,15 +97,22 @@ struct ThinArgs {
     int64_t cin_m, cin_n, cin_b;
     void* c;            // C'[i][j] at c + i c_m + j c_n (+ batch c_b)
     int64_t c_m, c_n, c_b;
-    float* part;        // [grid][2][m][TN] float32 partial tiles
+    float* part;        // [sk_blocks][2][m][TN] float32 partial tiles
+    // Schedule: the first sk_tiles tiles are split into equal runs of
+    // sk_units steps over blocks 0 .. sk_blocks - 1; each block then takes
+    // dp_rounds whole tiles, sk_tiles + blockIdx.x + j gridDim.x.
+    // (skipping tiles past all_tiles).
+    int64_t sk_tiles, sk_units, sk_blocks, dp_rounds, all_tiles;
 };
 
-template <typename T, bool KMAJOR, int R>
+template <typename T, bool KMAJOR, int R, int CB>
 struct Thin {
     using S = typename Elem<T>::storage;
     static constexpr bool k16 = sizeof(S) == 2;
     static constexpr int V = 16 / sizeof(S);               // elements per packet
-    static constexpr int NB = KMAJOR ? 4 : (k16 ? 8 : 4);  // MFMA column groups
+    // MFMA column groups of 16: CB with W K-major (chosen by the host from
+    // the product's width), fixed by the packet with W N-major.
+    static constexpr int NB = KMAJOR ? CB : (k16 ? 8 : 4);
     static constexpr int TN = 16 * NB;                     // tile columns
     // K-major W: a step gives each lane HALVES packets of a column, lane g
     // taking packets HALVES g .. HALVES g + HALVES - 1 of the step's k, so
@@ -118,16 +128,16 @@ struct Thin {
     // Steps a batch of loads, and blocks a CU the registers are sized for
     // (float32 K-major with 17-32 rows: one packet a step at two blocks a
     // CU, 32 x 11008 x 4096 in 47 us against 58 us at two and one block).
-    static constexpr int U = KMAJOR ? 1 : (k16 ? 1 : 8);
+    static constexpr int U = KMAJOR ? (HALVES == 2 ? 8 : 4) / (NB * HALVES) : (k16 ? 1 : 8);
     static constexpr int OCCUPANCY = (!k16 && KMAJOR && R == 2) ? 2 : 1;
     // X fragment: 8 (16-bit) or 4 (float32 K-major) consecutive k as one
     // packet, or one float.
     static constexpr bool kXPacket = k16 || KMAJOR;
 };
 
-template <typename T, bool KMAJOR, int R>
+template <typename T, bool KMAJOR, int R, int CB>
 struct StepData {
-    using P = Thin<T, KMAJOR, R>;
+    using P = Thin<T, KMAJOR, R, CB>;
     uint4 w[P::WL];
     typename std::conditional<P::kXPacket, uint4, float>::type x[R * P::XL];
 };
@@ -175,9 +185,9 @@ __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 }
 
 // A wave's view of one piece of a tile: its resources and per-lane offsets.
-template <typename T, bool KMAJOR, int R, bool XVEC>
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
 struct ThinWave {
-    using P = Thin<T, KMAJOR, R>;
+    using P = Thin<T, KMAJOR, R, CB>;
     using S = typename Elem<T>::storage;
     static constexpr int ES = sizeof(S);
     __amdgpu_buffer_rsrc_t wres, xres;
@@ -222,7 +232,7 @@ struct ThinWave {
     }
 
     // The loads of step s.
-    __device__ __forceinline__ void load(StepData<T, KMAJOR, R>& d, int64_t s) const {
+    __device__ __forceinline__ void load(StepData<T, KMAJOR, R, CB>& d, int64_t s) const {
         constexpr int V = P::V, H = P::XL;
         if constexpr (P::kXPacket) {
             // This lane's packets: k = kv[h] .. kv[h] + V - 1.
@@ -280,10 +290,10 @@ struct ThinWave {
     }
 };
 
-template <typename T, bool KMAJOR, int R>
-__device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d,
-                                         f32x4 (&acc)[R][Thin<T, KMAJOR, R>::NB]) {
-    using P = Thin<T, KMAJOR, R>;
+template <typename T, bool KMAJOR, int R, int CB>
+__device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R, CB>& d,
+                                         f32x4 (&acc)[R][Thin<T, KMAJOR, R, CB>::NB]) {
+    using P = Thin<T, KMAJOR, R, CB>;
     constexpr int H = P::XL;
     if constexpr (P::k16) {
         if constexpr (KMAJOR) {
@@ -329,25 +339,25 @@ __device__ __forceinline__ void mma_step(const StepData<T, KMAJOR, R>& d,
 
 // Steps [s, end) of one tile into acc: batches of U steps, the next batch's
 // loads issued before the current one's MFMAs (steps past `end` load zeros).
-template <typename T, bool KMAJOR, int R, bool XVEC>
-__device__ __forceinline__ void run_steps(const ThinWave<T, KMAJOR, R, XVEC>& wv, int64_t s, int64_t end,
-                                          f32x4 (&acc)[R][Thin<T, KMAJOR, R>::NB]) {
-    constexpr int U = Thin<T, KMAJOR, R>::U;
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
+__device__ __forceinline__ void run_steps(const ThinWave<T, KMAJOR, R, CB, XVEC>& wv, int64_t s, int64_t end,
+                                          f32x4 (&acc)[R][Thin<T, KMAJOR, R, CB>::NB]) {
+    constexpr int U = Thin<T, KMAJOR, R, CB>::U;
     if (s >= end) return;
-    StepData<T, KMAJOR, R> a[U], b[U];
+    StepData<T, KMAJOR, R, CB> a[U], b[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) wv.load(a[u], s + u);
     for (;;) {
 #pragma unroll
         for (int u = 0; u < U; ++u) wv.load(b[u], s + U + u);
 #pragma unroll
-        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R>(a[u], acc);
+        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R, CB>(a[u], acc);
         s += U;
         if (s >= end) break;
 #pragma unroll
         for (int u = 0; u < U; ++u) wv.load(a[u], s + U + u);
 #pragma unroll
-        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R>(b[u], acc);
+        for (int u = 0; u < U; ++u) mma_step<T, KMAJOR, R, CB>(b[u], acc);
         s += U;
         if (s >= end) break;
     }
@@ -371,10 +381,10 @@ __device__ __forceinline__ void store_c(const ThinArgs& p, int64_t bi, int64_t i
     static_cast<S*>(p.c)[bi * p.c_b + i * p.c_m + j * p.c_n] = Elem<T>::store(out);
 }
 
-template <typename T, bool KMAJOR, int R, bool XVEC>
-__global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void gemm_thin_kernel(
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
+__global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R, CB>::OCCUPANCY)) void gemm_thin_kernel(
     ThinArgs p) {
-    using P = Thin<T, KMAJOR, R>;
+    using P = Thin<T, KMAJOR, R, CB>;
     constexpr int NB = P::NB, TN = P::TN, E = R * NB * 4;
     constexpr int EPT = (16 * R * TN + kThinThreads - 1) / kThinThreads;  // fold elements a thread
     __shared__ float red[kThinWaves / 2][E][kWave];
@@ -382,13 +392,12 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
     __shared__ bool last;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int c = lane & 15, g = lane >> 4;
-    const int64_t blocks = gridDim.x;
-    const int64_t u_begin = static_cast<int64_t>(blockIdx.x) * p.units / blocks;
-    const int64_t u_end = (static_cast<int64_t>(blockIdx.x) + 1) * p.units / blocks;
-    for (int64_t u = u_begin; u < u_end;) {
-        const int64_t t = u / p.steps;  // tile, batch-major
-        const int64_t s0 = u - t * p.steps;
-        const int64_t s1 = std::min(p.steps, s0 + (u_end - u));
+    const int64_t blocks = p.sk_blocks;
+    const int64_t u_begin = blockIdx.x < blocks ? static_cast<int64_t>(blockIdx.x) * p.sk_units / blocks : 0;
+    const int64_t u_end = blockIdx.x < blocks ? (static_cast<int64_t>(blockIdx.x) + 1) * p.sk_units / blocks : 0;
+    // Steps [s0, s1) of tile t (batch-major).  first_piece: the block's
+    // first piece of its split run (its partial slot).
+    auto piece = [&](int64_t t, int64_t s0, int64_t s1, bool first_piece) {
         const int64_t bi = t / p.tiles, col0 = (t - bi * p.tiles) * TN;
         // This wave's run of the block's steps.
         const int64_t len = s1 - s0, q = (len + kThinWaves - 1) / kThinWaves;
@@ -399,9 +408,9 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[r][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if (ws0 < ws1) {
-            ThinWave<T, KMAJOR, R, XVEC> wv;
+            ThinWave<T, KMAJOR, R, CB, XVEC> wv;
             wv.init(p, bi, col0, ws0, ws1, lane);
-            run_steps<T, KMAJOR, R, XVEC>(wv, ws0, ws1, acc);
+            run_steps<T, KMAJOR, R, CB, XVEC>(wv, ws0, ws1, acc);
         }
         // Waves' sums in a fixed tree: (w0 + w2) + (w1 + w3).
 #pragma unroll
@@ -447,7 +456,7 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
         } else {
             // A piece of a tile shared with other blocks: this block's
             // partial goes to its slot (0 for its first piece, 1 for its last).
-            float* mine = p.part + (static_cast<int64_t>(blockIdx.x) * 2 + (u == u_begin ? 0 : 1)) * elems;
+            float* mine = p.part + (static_cast<int64_t>(blockIdx.x) * 2 + (first_piece ? 0 : 1)) * elems;
             for (int64_t e = tid; e < elems; e += kThinThreads) {
                 const int64_t i = e / TN, jl = e - i * TN;
                 __hip_atomic_store(mine + e, tile[i][jl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -456,8 +465,8 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
             // arrival; the last arrival's agent-scope loads read it there.
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            const int64_t first = block_of(t * p.steps, p.units, blocks);
-            const int64_t final_b = block_of((t + 1) * p.steps - 1, p.units, blocks);
+            const int64_t first = block_of(t * p.steps, p.sk_units, blocks);
+            const int64_t final_b = block_of((t + 1) * p.steps - 1, p.sk_units, blocks);
             if (tid == 0) {
                 unsigned int* ctr = &thin_counters[first * kCounterStride];
                 last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -478,7 +487,7 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
                     for (int d = 0; d < 4; ++d) {
                         const int64_t b = b0 + d;
                         // Tile t is block b's first piece when b starts inside it.
-                        const int slot = b * p.units / blocks >= tile_start ? 0 : 1;
+                        const int slot = b * p.sk_units / blocks >= tile_start ? 0 : 1;
                         const float* src = p.part + (b * 2 + slot) * elems;
 #pragma unroll
                         for (int q2 = 0; q2 < EPT; ++q2) {
@@ -505,56 +514,113 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R>::OCCUPANCY)) void
             }
         }
         __syncthreads();  // tile and red are reused by the next piece
+    };
+    // Split tiles first, so that their folds overlap the whole tiles other
+    // blocks are still streaming; whole tiles last.
+    for (int64_t u = u_begin; u < u_end;) {
+        const int64_t t = u / p.steps;
+        const int64_t s0 = u - t * p.steps;
+        const int64_t s1 = std::min(p.steps, s0 + (u_end - u));
+        piece(t, s0, s1, u == u_begin);
         u += s1 - s0;
+    }
+    for (int64_t j = 0; j < p.dp_rounds; ++j) {
+        const int64_t t = p.sk_tiles + blockIdx.x + j * static_cast<int64_t>(gridDim.x);
+        if (t < p.all_tiles) piece(t, 0, p.steps, false);
     }
 }
 
-template <typename T, bool KMAJOR, int R, bool XVEC>
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
 int blocks_per_cu() {
     static const int n = [] {
         int b = 0;
         TP_AMD_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &b, reinterpret_cast<const void*>(gemm_thin_kernel<T, KMAJOR, R, XVEC>), kThinThreads, 0));
+            &b, reinterpret_cast<const void*>(gemm_thin_kernel<T, KMAJOR, R, CB, XVEC>), kThinThreads, 0));
         return std::max(b, 1);
     }();
     return n;
 }
 
-template <typename T, bool KMAJOR, int R, bool XVEC>
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
+int64_t thin_slots(int device) {
+    return std::min<int64_t>(static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, CB, XVEC>()) * cu_count(device),
+                             kMaxThinBlocks);
+}
+
+// The schedule (see ThinArgs) over `slots` blocks resident at once.
+//   * At least a round of tiles: every block takes whole tiles, and the
+//     tiles left over from the last round (fewer than a round) are split
+//     over the blocks first.  Their folds then overlap the whole tiles other
+//     blocks are still streaming, and no fold remains at the end.
+//   * Fewer tiles than blocks: every tile is split, into pieces of at least
+//     kMinPieceBytes of W -- a tile cut into many small pieces pays for their
+//     fold (a write-through, an atomic and the reads, each a trip to the
+//     coherent level) more than they gain.
+template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
 void launch_kernel(ThinArgs q, int64_t batch, hipStream_t stream) {
-    using P = Thin<T, KMAJOR, R>;
+    using P = Thin<T, KMAJOR, R, CB>;
     int device = 0;
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     q.tiles = (q.n + P::TN - 1) / P::TN;
     q.steps = (q.k + P::STEP - 1) / P::STEP;
-    q.units = batch * q.tiles * q.steps;
-    // As many blocks as fit at once.  With fewer tiles than that, tiles are
-    // split, but into pieces of at least kMinPieceBytes of W: a tile split
-    // into many small pieces pays for their fold (a write-through, an atomic
-    // and the reads, each a trip to the coherent level) more than they gain.
-    const int64_t slots = std::min<int64_t>(
-        static_cast<int64_t>(blocks_per_cu<T, KMAJOR, R, XVEC>()) * cu_count(device), kMaxThinBlocks);
+    const int64_t slots = thin_slots<T, KMAJOR, R, CB, XVEC>(device);
     const int64_t tiles = batch * q.tiles;
-    const int64_t min_units = std::max<int64_t>(1, kMinPieceBytes / (P::STEP * P::TN * sizeof(typename Elem<T>::storage)));
-    const int64_t grid = std::min<int64_t>(slots, std::max<int64_t>(tiles, q.units / min_units));
-    Workspace ws;
-    // Partials exist only when some tile is split between blocks.
-    if (q.units % grid != 0 || (q.units / grid) % q.steps != 0) {
-        ws = Workspace(static_cast<size_t>(grid) * 2 * q.m * P::TN * sizeof(float), device);
-        q.part = static_cast<float*>(ws.get());
+    const int64_t step_bytes = P::STEP * P::TN * static_cast<int64_t>(sizeof(typename Elem<T>::storage));
+    int64_t grid;
+    q.all_tiles = tiles;
+    if (tiles >= slots && step_bytes * q.steps < kSplitTileBytes) {
+        // Small tiles: whole tiles dealt round the blocks (a fold would cost
+        // more than the last round's imbalance).
+        grid = slots;
+        q.sk_tiles = q.sk_units = q.sk_blocks = 0;
+        q.dp_rounds = (tiles + slots - 1) / slots;
+    } else if (tiles >= slots) {
+        grid = slots;
+        q.sk_tiles = tiles % slots;
+        q.dp_rounds = tiles / slots;
+        q.sk_units = q.sk_tiles * q.steps;
+        // The left-over tiles over every block, in pieces of at least
+        // kMinSplitBytes (the fold of a tile reads every piece).
+        q.sk_blocks = std::min(grid, std::max<int64_t>(q.sk_tiles, q.sk_units / std::max<int64_t>(1, kMinSplitBytes / step_bytes)));
     } else {
-        q.part = nullptr;
+        // Every tile split, over at most one block a CU for 16-bit types
+        // and two for float32: more blocks (more, smaller pieces, each
+        // folded) measured slower, e.g. bf16 1 x 4096 x 4096 10.5 us on one
+        // block a CU, 11.9 us on two; float32 1 x 11008 x 4096 35.3 us on
+        // two, 38.4 us on three.
+        q.sk_tiles = tiles;
+        q.dp_rounds = 0;
+        q.sk_units = tiles * q.steps;
+        const int64_t cap = std::min<int64_t>(slots, (P::k16 ? 1 : 2) * static_cast<int64_t>(cu_count(device)));
+        grid = std::min(cap, std::max<int64_t>(tiles, q.sk_units / std::max<int64_t>(1, kMinPieceBytes / step_bytes)));
+        q.sk_blocks = grid;
     }
-    gemm_thin_kernel<T, KMAJOR, R, XVEC><<<static_cast<unsigned>(grid), kThinThreads, 0, stream>>>(q);
+    Workspace ws;
+    q.part = nullptr;
+    // Partials exist only when some tile is split between blocks.
+    if (q.sk_blocks > 0 && (q.sk_units % q.sk_blocks != 0 || (q.sk_units / q.sk_blocks) % q.steps != 0)) {
+        ws = Workspace(static_cast<size_t>(q.sk_blocks) * 2 * q.m * P::TN * sizeof(float), device);
+        q.part = static_cast<float*>(ws.get());
+    }
+    gemm_thin_kernel<T, KMAJOR, R, CB, XVEC><<<static_cast<unsigned>(grid), kThinThreads, 0, stream>>>(q);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
+// Four column groups a wave with W K-major (64-wide tiles).  One group
+// (16-wide tiles, so that more products have a whole tile for every block)
+// measured slower: bf16 1 x 4096 x 11008 21.3 -> 23.1 us, 32 rows
+// 28.9 -> 42.4 us.
+constexpr int kColumnGroups = 4;
+
 template <typename T, bool KMAJOR>
 void launch_rows(const ThinArgs& q, bool xvec, int64_t batch, hipStream_t stream) {
+    constexpr int CB = kColumnGroups;
     if (q.m > 16) {
-        xvec ? launch_kernel<T, KMAJOR, 2, true>(q, batch, stream) : launch_kernel<T, KMAJOR, 2, false>(q, batch, stream);
+        xvec ? launch_kernel<T, KMAJOR, 2, CB, true>(q, batch, stream)
+             : launch_kernel<T, KMAJOR, 2, CB, false>(q, batch, stream);
     } else {
-        xvec ? launch_kernel<T, KMAJOR, 1, true>(q, batch, stream) : launch_kernel<T, KMAJOR, 1, false>(q, batch, stream);
+        xvec ? launch_kernel<T, KMAJOR, 1, CB, true>(q, batch, stream)
+             : launch_kernel<T, KMAJOR, 1, CB, false>(q, batch, stream);
     }
 }
 
