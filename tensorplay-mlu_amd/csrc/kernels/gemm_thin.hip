@@ -32,15 +32,17 @@
 //
 // Fragments (lane l, c = l % 16, g = l / 16; MFMA output lane l holds rows
 // 4g..4g+3 of column c):
-//   * 16-bit, W K-major: v_mfma_f32_16x16x32; lane l loads W column
-//     (tile column 16 cb + c), k = k0 + 8g .. +7, one 16-byte packet, and the
-//     same k of X row c: the fragment needs no rearranging.
+//   * 16-bit, W K-major: v_mfma_f32_16x16x32; lane l loads two 16-byte
+//     packets of W column 16 cb + c, k = k0 + 16g .. +15, back to back,
+//     and the same k of X row c, one MFMA a packet: the fragments need no
+//     rearranging.
 //   * 16-bit, W N-major: a lane loads 8 consecutive columns 8c .. 8c+7 at the
 //     8 rows k0 + 8g + i and transposes the 8 x 8 block in registers; MFMA j
 //     then multiplies tile columns 8c + j (c = 0..15).
 //   * float32, W K-major: v_mfma_f32_16x16x4_f32; a 16-byte packet gives a
-//     lane k = k0 + 4g .. +3 of one column, fed to 4 MFMAs (MFMA e takes
-//     k0 + 4g + e from X and W alike).
+//     lane 4 consecutive k of one column, fed to 4 MFMAs (MFMA e takes the
+//     packet's k e from X and W alike); two packets a step as for 16-bit,
+//     one with 17-32 thin rows.
 //   * float32, W N-major: a lane loads 4 consecutive columns 4c .. 4c+3 of
 //     row k0 + g; MFMA j multiplies tile columns 4c + j.
 // The sum pairs X and W elements of the same k in every case, whatever
