@@ -93,12 +93,30 @@ __device__ __forceinline__ float erfc_fit(float t) {
     return fmaf(p, t, -1.26551223f);
 }
 
-// Normal CDF Phi(x) = erfc(-x / sqrt(2)) / 2 on the hardware exponential.
+// The same form with a degree-5 P, enough for a 16-bit result: fitted here
+// (least squares on 2000 Chebyshev nodes, reweighted towards the largest
+// errors) to log(erfcx(z) / t) for z in [0, 9.5], where erfc(z) reaches
+// bfloat16's smallest values; erfc's relative error is at most 7.6e-6
+// (degree 9: 1.2e-7), far under half a 16-bit ulp.  Four fewer FMAs a value,
+// on an operator whose VALU work otherwise exceeds its memory time.
+__device__ __forceinline__ float erfc_fit5(float t) {
+    float p = 0.22879168f;
+    p = fmaf(p, t, -0.70919508f);
+    p = fmaf(p, t, 0.47449806f);
+    p = fmaf(p, t, 0.25444061f);
+    p = fmaf(p, t, 1.01801419f);
+    return fmaf(p, t, -1.26654184f);
+}
+
+// Normal CDF Phi(x) = erfc(-x / sqrt(2)) / 2 on the hardware exponential,
+// for 16-bit results.  (The derivative keeps the degree-9 P: near its zero
+// at x = -0.75, cdf + x pdf cancels, and the degree-5 error grew to 21 fp16
+// ulps there in a float32 emulation.)
 __device__ __forceinline__ float phi_fast(float x) {
     const float z = x * kSqrt1_2;  // -(-x / sqrt 2)
     const float az = fabsf(z);
     const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, az, 1.0f));
-    const float c = t * exp_fast(fmaf(-az, az, erfc_fit(t)));  // erfc(|z|)
+    const float c = t * exp_fast(fmaf(-az, az, erfc_fit5(t)));  // erfc(|z|)
     return z >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
 }
 
