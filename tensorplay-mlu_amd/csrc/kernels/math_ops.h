@@ -93,31 +93,32 @@ __device__ __forceinline__ float erfc_fit(float t) {
     return fmaf(p, t, -1.26551223f);
 }
 
-// The same form with a degree-5 P, enough for a 16-bit result: fitted here
-// (least squares on 2000 Chebyshev nodes, reweighted towards the largest
-// errors) to log(erfcx(z) / t) for z in [0, 9.5], where erfc(z) reaches
-// bfloat16's smallest values; erfc's relative error is at most 7.6e-6
-// (degree 9: 1.2e-7), far under half a 16-bit ulp.  Four fewer FMAs a value,
-// on an operator whose VALU work otherwise exceeds its memory time.
-__device__ __forceinline__ float erfc_fit5(float t) {
-    float p = 0.22879168f;
-    p = fmaf(p, t, -0.70919508f);
-    p = fmaf(p, t, 0.47449806f);
-    p = fmaf(p, t, 0.25444061f);
-    p = fmaf(p, t, 1.01801419f);
-    return fmaf(p, t, -1.26654184f);
-}
-
-// Normal CDF Phi(x) = erfc(-x / sqrt(2)) / 2 on the hardware exponential,
-// for 16-bit results.  (The derivative keeps the degree-9 P: near its zero
-// at x = -0.75, cdf + x pdf cancels, and the degree-5 error grew to 21 fp16
-// ulps there in a float32 emulation.)
-__device__ __forceinline__ float phi_fast(float x) {
-    const float z = x * kSqrt1_2;  // -(-x / sqrt 2)
-    const float az = fabsf(z);
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, az, 1.0f));
-    const float c = t * exp_fast(fmaf(-az, az, erfc_fit5(t)));  // erfc(|z|)
-    return z >= 0.0f ? fmaf(-0.5f, c, 1.0f) : 0.5f * c;
+// x Phi(x) for a 16-bit result.  Phi(x) = 1 - q (x >= 0) or q (x < 0) with
+// q = erfc(|x| / sqrt 2) / 2 = t e^(-x^2 / 2 + P(t)) / 2 and
+// t = 1 / (1 + |x| / (2 sqrt 2)), P of degree 5 fitted here (least squares
+// on 2000 Chebyshev nodes, reweighted towards the largest errors) to
+// log(erfcx(z) / t) for z = |x| / sqrt 2 in [0, 9.5], where erfc reaches
+// bfloat16's smallest values: erfc's relative error is at most 7.6e-6
+// (degree 9: 1.2e-7), far under half a 16-bit ulp.  The exponential runs as
+// h^2 with h = 2^(-(x k)^2 + P'(t)), k^2 = log2(e) / 4 and P' = (P log2(e)
+// - 1) / 2 (the factor 1/2 folded in): h stays normal where q is
+// subnormal.  18 VALU operations a value against 26 for x * phi(x) on the
+// degree-9 P; an operator whose VALU work otherwise exceeds its memory time.
+// (The derivative keeps the degree-9 P: near its zero at x = -0.75,
+// cdf + x pdf cancels, and a degree-5 P gave 21 fp16 ulps there in a float32
+// emulation.)
+__device__ __forceinline__ float gelu16(float x) {
+    const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), 0.35355339f, 1.0f));  // 1 / (2 sqrt 2)
+    const float xs = x * 0.60056120f;                                          // sqrt(log2(e) / 4)
+    float p = 0.16503832f;
+    p = fmaf(p, t, -0.51157612f);
+    p = fmaf(p, t, 0.34227800f);
+    p = fmaf(p, t, 0.18354011f);
+    p = fmaf(p, t, 0.73434204f);
+    p = fmaf(p, t, -1.41361678f);
+    const float h = __builtin_amdgcn_exp2f(fmaf(-xs, xs, p));
+    const float q = t * (h * h);
+    return x * (x >= 0.0f ? 1.0f - q : q);
 }
 
 // Phi(x) and the density phi(x) = e^(-x^2/2) / sqrt(2 pi) together: with
@@ -227,7 +228,8 @@ struct UnaryFn {
         else if constexpr (OP == TP_AMD_UNARY_SILU) {
             return FAST ? x * sigmoid_fast(x) : x / (1.0f + expf(-x));
         } else if constexpr (OP == TP_AMD_UNARY_GELU) {
-            return x * (FAST ? phi_fast(x) : normal_f32<false>(x, nullptr));
+            if constexpr (FAST) return gelu16(x);
+            else return x * normal_f32<false>(x, nullptr);
         } else {
             if constexpr (FAST) {
                 const float u = kSqrt2OverPi * (x + kGeluTanhC * x * x * x);
