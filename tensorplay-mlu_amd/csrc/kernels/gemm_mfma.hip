@@ -1163,6 +1163,15 @@ constexpr double kRepackMinMacs = double(int64_t(1) << 22);
 
 void check_status(int status) { TP_AMD_CHECK(status == 0, last_error()); }
 
+template <typename T>
+struct DtypeOf;
+template <>
+struct DtypeOf<float> { static constexpr int value = TP_AMD_FLOAT32; };
+template <>
+struct DtypeOf<bf16_t> { static constexpr int value = TP_AMD_BFLOAT16; };
+template <>
+struct DtypeOf<f16_t> { static constexpr int value = TP_AMD_FLOAT16; };
+
 // A K-major source in one pass: dst row q (of bs x rows) = the source row
 // (b, r) = (q / rows, q % rows) at src + b stride + r ld, elements 0..k, then
 // zeros to kp.  A thread writes one 16-byte packet (kp is a whole number of
@@ -1256,7 +1265,8 @@ void launch_repacked(const GemmArgs& p, hipStream_t stream) {
         q.stride_b = p.stride_b == 0 ? 0 : p.n * kp;
         q.trans_b = true;
     }
-    launch_mfma<T>(q, stream);
+    // A thin product reads its repacked operand through the thin kernel.
+    if (!launch_gemm_thin(DtypeOf<T>::value, q, stream)) launch_mfma<T>(q, stream);
 }
 
 template <typename T>
