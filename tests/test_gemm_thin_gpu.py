@@ -169,3 +169,16 @@ def test_thin_nan_and_inf(dev, ops, orc, dtype, tb):
     inf = np.isinf(want)
     assert np.array_equal(np.isinf(got), inf), "infinities in other places"
     assert np.array_equal(got[inf], want[inf]), "signs of the infinities"
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
+def test_thin_after_repack(dev, ops, orc, dtype):
+    """x [3, 2048] @ W [2048, 1001]: W row-major with an odd leading
+    dimension, which no kernel reads in 16-byte packets, is copied K-major
+    and then multiplied by the thin kernel; against float64."""
+    g = np.random.default_rng(11)
+    x = orc.from_float(g.standard_normal((3, 2048)).astype(np.float32), dtype)
+    w = orc.from_float(g.standard_normal((2048, 1001)).astype(np.float32), dtype)
+    got = ops.mm(dev.from_numpy(x, dtype=dtype), dev.from_numpy(w, dtype=dtype)).numpy()
+    want = orc.to_float(x, dtype).astype(np.float64) @ orc.to_float(w, dtype).astype(np.float64)
+    _check(orc, got, want, dtype, "thin product of a repacked operand")
