@@ -28,7 +28,7 @@ struct GemmArgs {
 template <typename T>
 void launch_gemm_general(const GemmArgs& p, hipStream_t stream);
 
-// Products with at most 32 rows or 32 columns whose large operand the
+// Products with at most 64 rows or 64 columns whose large operand the
 // matrix cores can read in place (gemm_thin.hip); false when not eligible.
 bool launch_gemm_thin(int dtype, const GemmArgs& p, hipStream_t stream);
 

@@ -1,5 +1,5 @@
 // Thin products on the matrix cores (gfx950): C = alpha A B + beta Cin
-// where one side of C is at most 32 long -- a decode step's x W^T, a
+// where one side of C is at most 64 long -- a decode step's x W^T, a
 // matrix-vector product, the dX = dY W of an LM head, attention over one
 // query.  Such a product reads its large operand once and does almost no
 // arithmetic per byte, so it is bound by HBM; the tiled kernels
@@ -7,7 +7,7 @@
 // all of K on one CU and reach a fifth of the bandwidth.
 //
 // Normal form.  The host turns every eligible product into
-//   C'[i][j] = sum_k X[i][k] W[k][j],  i < m <= 32 ("thin" rows),
+//   C'[i][j] = sum_k X[i][k] W[k][j],  i < m <= 64 ("thin" rows),
 // X the small operand (any strides), W the wide one, stored K-major
 // (element (k, j) at w + j ld + k: a Linear weight, or A of a product with
 // few columns) or N-major (at w + k ld + j: a [K, N] row-major matrix).
@@ -22,7 +22,7 @@
 // overlap the whole tiles still streaming.  With fewer tiles than that,
 // every tile is split, into pieces of at least 64 KiB of W.  Within a
 // block's piece of a tile the four waves take consecutive runs of steps,
-// each with 16 x 16 MFMAs (the thin rows padded with zeros to 16 or 32),
+// each with 16 x 16 MFMAs (the thin rows padded with zeros to 16, 32 or 64),
 // the next batch of loads in flight; the waves' sums are added in LDS in a
 // fixed tree.  A tile that one block covers whole is written at once.  A
 // tile split between blocks gets a float32 partial from each, stored
@@ -42,7 +42,7 @@
 //   * float32, W K-major: v_mfma_f32_16x16x4_f32; a 16-byte packet gives a
 //     lane 4 consecutive k of one column, fed to 4 MFMAs (MFMA e takes the
 //     packet's k e from X and W alike); two packets a step as for 16-bit,
-//     one with 17-32 thin rows.
+//     one with more than 16 thin rows.
 //   * float32, W N-major: a lane loads 4 consecutive columns 4c .. 4c+3 of
 //     row k0 + g; MFMA j multiplies tile columns 4c + j.
 // The sum pairs X and W elements of the same k in every case, whatever
@@ -71,7 +71,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThinWaves = 4;
 constexpr int kThinThreads = kThinWaves * kWave;
-constexpr int64_t kThinMaxRows = 32;
+constexpr int64_t kThinMaxRows = 64;
 // One arrival counter per tile split between blocks, indexed by the first
 // block that covers the tile (unique among split tiles), each on a 128-byte
 // line of its own: atomics on one line serialize.
@@ -81,13 +81,13 @@ constexpr int64_t kMinPieceBytes = int64_t(64) << 10;
 constexpr int64_t kMinSplitBytes = int64_t(16) << 10;
 constexpr int64_t kSplitTileBytes = int64_t(256) << 10;
 // Least bytes of the wide operand for which a product takes this kernel:
-// up to 16 thin rows, and 17 to 32.
+// up to 16 thin rows, and more.
 constexpr int64_t kMinWideBytes1 = int64_t(1) << 20;
 constexpr int64_t kMinWideBytes2 = int64_t(8) << 20;
 __device__ unsigned int thin_counters[kMaxThinBlocks * kCounterStride];
 
 struct ThinArgs {
-    int64_t m, n, k;    // thin rows (<= 32), columns, depth
+    int64_t m, n, k;    // thin rows (<= 64), columns, depth
     int64_t tiles;      // column tiles of one batch entry
     int64_t steps;      // K steps of a tile
     float alpha, beta;
@@ -122,8 +122,8 @@ struct Thin {
     // cover whole 128-byte lines (with one packet a lane, the two halves of
     // a line were requested a step apart and some lines were fetched twice:
     // FETCH_SIZE 1.116x the operand for bf16 1 x 4096 x 11008).  float32
-    // with 17-32 rows keeps one packet, for registers.
-    static constexpr int HALVES = KMAJOR && !(!k16 && R == 2) ? 2 : 1;
+    // with more than 16 rows keeps one packet, for registers.
+    static constexpr int HALVES = KMAJOR && !(!k16 && R >= 2) ? 2 : 1;
     static constexpr int STEP = KMAJOR ? 4 * V * HALVES : (k16 ? 32 : 4);  // K per step
     static constexpr int WL = KMAJOR ? NB * HALVES : (k16 ? 8 : 1);       // W packets a step
     static constexpr int XL = KMAJOR ? HALVES : 1;                        // X fragments a row
@@ -387,9 +387,14 @@ template <typename T, bool KMAJOR, int R, int CB, bool XVEC>
 __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R, CB>::OCCUPANCY)) void gemm_thin_kernel(
     ThinArgs p) {
     using P = Thin<T, KMAJOR, R, CB>;
-    constexpr int NB = P::NB, TN = P::TN, E = R * NB * 4;
-    constexpr int EPT = (16 * R * TN + kThinThreads - 1) / kThinThreads;  // fold elements a thread
-    __shared__ float red[kThinWaves / 2][E][kWave];
+    constexpr int NB = P::NB, TN = P::TN;
+    // Row groups reduced together (the LDS tree's slots hold RC of them), and
+    // fold elements a thread, taken FC at a time.
+    constexpr int RC = R < 16 / NB ? R : 16 / NB;
+    constexpr int EPT = (16 * R * TN + kThinThreads - 1) / kThinThreads;
+    constexpr int FC = EPT < 8 ? EPT : 8;
+    static_assert(R % RC == 0 && EPT % FC == 0, "row groups and fold chunks divide evenly");
+    __shared__ float red[kThinWaves / 2][RC * NB * 4][kWave];
     __shared__ float tile[16 * R][TN + 1];
     __shared__ bool last;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -414,27 +419,32 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R, CB>::OCCUPANCY)) 
             wv.init(p, bi, col0, ws0, ws1, lane);
             run_steps<T, KMAJOR, R, CB, XVEC>(wv, ws0, ws1, acc);
         }
-        // Waves' sums in a fixed tree: (w0 + w2) + (w1 + w3).
+        // Waves' sums in a fixed tree, (w0 + w2) + (w1 + w3), RC row groups
+        // at a time.
 #pragma unroll
-        for (int half = kThinWaves / 2; half >= 1; half /= 2) {
-            if (wave >= half && wave < 2 * half) {
+        for (int r0 = 0; r0 < R; r0 += RC) {
 #pragma unroll
-                for (int r = 0; r < R; ++r)
+            for (int half = kThinWaves / 2; half >= 1; half /= 2) {
+                if (wave >= half && wave < 2 * half) {
 #pragma unroll
-                    for (int j = 0; j < NB; ++j)
+                    for (int r = 0; r < RC; ++r)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) red[wave - half][(r * NB + j) * 4 + i][lane] = acc[r][j][i];
+                        for (int j = 0; j < NB; ++j)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                red[wave - half][(r * NB + j) * 4 + i][lane] = acc[r0 + r][j][i];
+                }
+                __syncthreads();
+                if (wave < half) {
+#pragma unroll
+                    for (int r = 0; r < RC; ++r)
+#pragma unroll
+                        for (int j = 0; j < NB; ++j)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[r0 + r][j][i] += red[wave][(r * NB + j) * 4 + i][lane];
+                }
+                __syncthreads();
             }
-            __syncthreads();
-            if (wave < half) {
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-#pragma unroll
-                    for (int j = 0; j < NB; ++j)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[r][j][i] += red[wave][(r * NB + j) * 4 + i][lane];
-            }
-            __syncthreads();
         }
         if (wave == 0) {
 #pragma unroll
@@ -480,37 +490,41 @@ __global__ __launch_bounds__(kThinThreads, (Thin<T, KMAJOR, R, CB>::OCCUPANCY)) 
                 // Partials of blocks first..final_b added in block order; each
                 // thread's elements of four blocks are loaded before any add.
                 const int64_t tile_start = t * p.steps;
-                float v[EPT];
+                for (int e0 = 0; e0 < EPT; e0 += FC) {
+                    if (static_cast<int64_t>(e0) * kThinThreads >= elems) break;
+                    float v[FC];
 #pragma unroll
-                for (int q2 = 0; q2 < EPT; ++q2) v[q2] = 0.0f;
-                for (int64_t b0 = first; b0 <= final_b; b0 += 4) {
-                    float h[4][EPT];
+                    for (int q2 = 0; q2 < FC; ++q2) v[q2] = 0.0f;
+                    for (int64_t b0 = first; b0 <= final_b; b0 += 4) {
+                        float h[4][FC];
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const int64_t b = b0 + d;
-                        // Tile t is block b's first piece when b starts inside it.
-                        const int slot = b * p.sk_units / blocks >= tile_start ? 0 : 1;
-                        const float* src = p.part + (b * 2 + slot) * elems;
+                        for (int d = 0; d < 4; ++d) {
+                            const int64_t b = b0 + d;
+                            // Tile t is block b's first piece when b starts inside it.
+                            const int slot = b * p.sk_units / blocks >= tile_start ? 0 : 1;
+                            const float* src = p.part + (b * 2 + slot) * elems;
 #pragma unroll
-                        for (int q2 = 0; q2 < EPT; ++q2) {
-                            const int64_t e = tid + q2 * kThinThreads;
-                            h[d][q2] = b <= final_b && e < elems
-                                           ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                           : 0.0f;
+                            for (int q2 = 0; q2 < FC; ++q2) {
+                                const int64_t e = tid + (e0 + q2) * kThinThreads;
+                                h[d][q2] = b <= final_b && e < elems
+                                               ? __hip_atomic_load(src + e, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT)
+                                               : 0.0f;
+                            }
                         }
+#pragma unroll
+                        for (int d = 0; d < 4; ++d)
+#pragma unroll
+                            for (int q2 = 0; q2 < FC; ++q2)
+                                if (b0 + d <= final_b) v[q2] += h[d][q2];
                     }
 #pragma unroll
-                    for (int d = 0; d < 4; ++d)
-#pragma unroll
-                        for (int q2 = 0; q2 < EPT; ++q2)
-                            if (b0 + d <= final_b) v[q2] += h[d][q2];
-                }
-#pragma unroll
-                for (int q2 = 0; q2 < EPT; ++q2) {
-                    const int64_t e = tid + q2 * kThinThreads;
-                    if (e < elems) {
-                        const int64_t i = e / TN, jl = e - i * TN;
-                        if (col0 + jl < p.n) store_c<T>(p, bi, i, col0 + jl, v[q2]);
+                    for (int q2 = 0; q2 < FC; ++q2) {
+                        const int64_t e = tid + (e0 + q2) * kThinThreads;
+                        if (e < elems) {
+                            const int64_t i = e / TN, jl = e - i * TN;
+                            if (col0 + jl < p.n) store_c<T>(p, bi, i, col0 + jl, v[q2]);
+                        }
                     }
                 }
             }
@@ -614,15 +628,30 @@ void launch_kernel(ThinArgs q, int64_t batch, hipStream_t stream) {
 // 28.9 -> 42.4 us.
 constexpr int kColumnGroups = 4;
 
+template <typename T, bool KMAJOR, int R>
+void launch_x(const ThinArgs& q, bool xvec, int64_t batch, hipStream_t stream) {
+    constexpr int CB = kColumnGroups;
+    xvec ? launch_kernel<T, KMAJOR, R, CB, true>(q, batch, stream)
+         : launch_kernel<T, KMAJOR, R, CB, false>(q, batch, stream);
+}
+
+// Most thin rows a variant takes (rows are padded to 16, 32 or 64).  W
+// N-major in 16-bit types holds 8 column groups a wave and spills from 64
+// rows on.  128 rows (8 row groups) compiled without spills for W K-major
+// but ran no faster than the tiled kernels (bf16 128 x 4096 x 11008 64.8 us
+// against 57.8 us): every wave reads its own 128 rows of X for 64 columns
+// of W, twice the bytes of W, from L2.
+int thin_max_rows(bool k16, bool kmajor) { return !kmajor && k16 ? 32 : 64; }
+
 template <typename T, bool KMAJOR>
 void launch_rows(const ThinArgs& q, bool xvec, int64_t batch, hipStream_t stream) {
-    constexpr int CB = kColumnGroups;
-    if (q.m > 16) {
-        xvec ? launch_kernel<T, KMAJOR, 2, CB, true>(q, batch, stream)
-             : launch_kernel<T, KMAJOR, 2, CB, false>(q, batch, stream);
+    constexpr bool k16 = sizeof(typename Elem<T>::storage) == 2;
+    if (q.m > 32) {
+        if constexpr (KMAJOR || !k16) launch_x<T, KMAJOR, 4>(q, xvec, batch, stream);
+    } else if (q.m > 16) {
+        launch_x<T, KMAJOR, 2>(q, xvec, batch, stream);
     } else {
-        xvec ? launch_kernel<T, KMAJOR, 1, CB, true>(q, batch, stream)
-             : launch_kernel<T, KMAJOR, 1, CB, false>(q, batch, stream);
+        launch_x<T, KMAJOR, 1>(q, xvec, batch, stream);
     }
 }
 
@@ -698,6 +727,7 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
     if (wbytes < (q.m > 16 ? kMinWideBytes2 : kMinWideBytes1)) return false;
     const bool xvec = q.x_k == 1 && q.k % V == 0 && aligned16(q.x) && (q.m == 1 || q.x_m % V == 0) &&
                       (p.batch == 1 || q.x_b % V == 0);
+    if (q.m > thin_max_rows(sizeof(S) == 2, kmajor)) return false;
     if (kmajor) {
         launch_rows<T, true>(q, xvec, p.batch, stream);
     } else {

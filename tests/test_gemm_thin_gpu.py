@@ -1,4 +1,4 @@
-"""Thin products (at most 32 rows or 32 columns of C) on the GPU against the
+"""Thin products (at most 64 rows or 64 columns of C) on the GPU against the
 float64 product of the same stored operands: the decode-step shapes of a
 Linear layer, a matrix-vector product and an LM head, which run on their
 own kernel (stream-K over column tiles, 16 x 16 MFMAs, partials of tiles
@@ -91,10 +91,27 @@ def test_thin_layouts(amd, dev, orc, dtype, ta, tb, m, n, k):
     _check(orc, got[0], want[0], dtype, f"thin {m}x{n}x{k} ta={ta} tb={tb}")
 
 
+# 33 to 64 thin rows (row groups of 64): W K-major and float32 W N-major;
+# 16-bit W N-major past 32 rows, and anything past 64, goes to the tiled
+# kernels.  Checked in the four layouts like the shapes above.
+WIDE = [(40, 4104, 1024), (64, 2056, 2048), (65, 1032, 4096), (100, 4104, 1024)]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("m,n,k", WIDE + [(n, m, k) for (m, n, k) in WIDE],
+                         ids=[f"{m}x{n}x{k}" for (m, n, k) in WIDE] + [f"{n}x{m}x{k}" for (m, n, k) in WIDE])
+def test_thin_up_to_128_rows(amd, dev, orc, dtype, ta, tb, m, n, k):
+    lib = amd.load()
+    (got,), want = _run(lib, dev, orc, dtype, 1, m, n, k, ta, tb)
+    _check(orc, got[0], want[0], dtype, f"thin {m}x{n}x{k} ta={ta} tb={tb}")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)], ids=["NN", "NT", "TT"])
 @pytest.mark.parametrize("cin_kind", ["bias-row", "full"])
-@pytest.mark.parametrize("m,n,k", [(1, 1000, 1024), (24, 1040, 4096), (1032, 9, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 1024), (24, 1040, 4096), (1032, 9, 512), (96, 2056, 2048)])
 def test_thin_epilogue_batched(amd, dev, orc, dtype, ta, tb, cin_kind, m, n, k):
     """alpha = 0.5 and beta = 2 with a per-column bias or a full Cin, a
     batch of 3 (its B shared by the batch, stride 0, in the bias case), and
