@@ -261,7 +261,9 @@ __device__ __forceinline__ void tile_coords(int bid, int grid_m, int grid_n, int
     pn = (pid % in_group) / size_m;
 }
 
-template <typename T, bool A_KMAJOR, bool B_KMAJOR, int BM, int BN, int WM, int WN>
+// F32OUT: C is float32 (split-K partials of a 16-bit product), written as
+// alpha acc with no Cin.
+template <typename T, bool A_KMAJOR, bool B_KMAJOR, int BM, int BN, int WM, int WN, bool F32OUT = false>
 __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) {
     using S = typename Elem<T>::storage;
     constexpr int THREADS = WM * WN * kWave;
@@ -372,6 +374,25 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
 
         // Epilogue: lane holds column l32 of each 32 x 32 tile, rows
         // 8 * (e / 4) + 4 * half + e % 4 for accumulator element e.
+        if constexpr (F32OUT) {
+            float* C = static_cast<float*>(p.c) + bi * p.stride_c;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int64_t col = n0 + wn * kWaveN + j * 32 + l32;
+                    const int64_t rbase = m0 + wm * kWaveM + i * 32 + 4 * half;
+                    if (col >= p.n) continue;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t row = rbase + 8 * g + r;
+                            if (row < p.m) C[row * p.ldc + col] = p.alpha * acc[i][j][4 * g + r];
+                        }
+                }
+            return;
+        }
         S* C = static_cast<S*>(p.c) + bi * p.stride_c;
         const S* Cin = static_cast<const S*>(p.cin);
         if (p.trans_c) {
@@ -966,25 +987,25 @@ bool mfma_eligible(const GemmArgs& p) {
            operand_ok<T>(p.b, p.ldb, p.stride_b, p.trans_b, p.n, p.k) && tiles_fit(p);
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, bool F32OUT = false>
 void launch_chunk(const GemmArgs& p, hipStream_t stream) {
     constexpr int THREADS = WM * WN * kWave;
     const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
     const dim3 grid(static_cast<unsigned>(tiles), 1u, static_cast<unsigned>(p.batch));
     const bool a_kmajor = !p.trans_a, b_kmajor = p.trans_b;
     if (a_kmajor && b_kmajor) {
-        gemm_mfma_kernel<T, true, true, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+        gemm_mfma_kernel<T, true, true, BM, BN, WM, WN, F32OUT><<<grid, THREADS, 0, stream>>>(p);
     } else if (a_kmajor) {
-        gemm_mfma_kernel<T, true, false, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+        gemm_mfma_kernel<T, true, false, BM, BN, WM, WN, F32OUT><<<grid, THREADS, 0, stream>>>(p);
     } else if (b_kmajor) {
-        gemm_mfma_kernel<T, false, true, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+        gemm_mfma_kernel<T, false, true, BM, BN, WM, WN, F32OUT><<<grid, THREADS, 0, stream>>>(p);
     } else {
-        gemm_mfma_kernel<T, false, false, BM, BN, WM, WN><<<grid, THREADS, 0, stream>>>(p);
+        gemm_mfma_kernel<T, false, false, BM, BN, WM, WN, F32OUT><<<grid, THREADS, 0, stream>>>(p);
     }
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, bool F32OUT = false>
 void launch_config(const GemmArgs& whole, hipStream_t stream) {
     constexpr int64_t kMaxZ = 65535;
     using S = typename Elem<T>::storage;
@@ -993,9 +1014,10 @@ void launch_config(const GemmArgs& whole, hipStream_t stream) {
         p.batch = whole.batch - b0 < kMaxZ ? whole.batch - b0 : kMaxZ;
         p.a = static_cast<const S*>(whole.a) + b0 * whole.stride_a;
         p.b = static_cast<const S*>(whole.b) + b0 * whole.stride_b;
-        p.c = static_cast<S*>(whole.c) + b0 * whole.stride_c;
+        p.c = F32OUT ? static_cast<void*>(static_cast<float*>(whole.c) + b0 * whole.stride_c)
+                     : static_cast<void*>(static_cast<S*>(whole.c) + b0 * whole.stride_c);
         if (whole.cin != nullptr) p.cin = static_cast<const S*>(whole.cin) + b0 * whole.cin_stride_b;
-        launch_chunk<T, BM, BN, WM, WN>(p, stream);
+        launch_chunk<T, BM, BN, WM, WN, F32OUT>(p, stream);
     }
 }
 // Split K for float32 products with too few 128 x 128 tiles to fill the
@@ -1009,11 +1031,11 @@ void launch_config(const GemmArgs& whole, hipStream_t stream) {
 // slice keeps at least 128 of K, a multiple of the kernel's BK = 32.
 constexpr int kFinishBlock = 256;
 
-int splitk_slices(const GemmArgs& p, int cus, int tile = 128, int min_k = 128) {
+int splitk_slices(const GemmArgs& p, int cus, int tile = 128, int min_k = 128, int bk = 32) {
     if (p.batch != 1) return 1;
     const int64_t tiles = ((p.m + tile - 1) / tile) * ((p.n + tile - 1) / tile);
     int s = 1;
-    while (tiles * s * 2 <= cus && p.k % (s * 2 * 32) == 0 && p.k / (s * 2) >= min_k) s *= 2;
+    while (tiles * s * 2 <= cus && p.k % (s * 2 * bk) == 0 && p.k / (s * 2) >= min_k) s *= 2;
     return s;
 }
 
@@ -1061,6 +1083,56 @@ void launch_splitk(const GemmArgs& p, int slices, hipStream_t stream, int device
     splitk_finish_kernel<<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
         static_cast<const float*>(ws.get()), slices, p.m, p.n, p.alpha, p.beta,
         static_cast<const float*>(p.cin), p.cin_rs, p.cin_cs, static_cast<float*>(p.c), p.ldc);
+    TP_AMD_HIP_CHECK(hipGetLastError());
+}
+
+// The same split for 16-bit products: the slices write float32 partials
+// (the tile kernel's F32OUT epilogue) and the finish adds them in slice
+// order and rounds once to the output type.
+template <typename T>
+__global__ __launch_bounds__(kFinishBlock) void splitk_finish16_kernel(
+    const float* part, int slices, int64_t m, int64_t n, float alpha, float beta,
+    const typename Elem<T>::storage* cin, int64_t cin_rs, int64_t cin_cs, typename Elem<T>::storage* c,
+    int64_t ldc) {
+    const int64_t mn = m * n;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kFinishBlock + threadIdx.x; i < mn;
+         i += static_cast<int64_t>(gridDim.x) * kFinishBlock) {
+        float acc = part[i];
+        for (int s = 1; s < slices; ++s) acc += part[s * mn + i];
+        const int64_t r = i / n, col = i % n;
+        float v;
+        if (beta == 0.0f) {
+            v = alpha * acc;
+        } else if (cin_rs == 0) {
+            v = fmaf(alpha, acc, beta * Elem<T>::load(cin[col * cin_cs]));
+        } else {
+            v = fmaf(beta, Elem<T>::load(cin[r * cin_rs + col * cin_cs]), alpha * acc);
+        }
+        c[r * ldc + col] = Elem<T>::store(v);
+    }
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+void launch_splitk16(const GemmArgs& p, int slices, hipStream_t stream, int device) {
+    using S = typename Elem<T>::storage;
+    const int64_t mn = p.m * p.n;
+    Workspace ws(static_cast<size_t>(slices * mn) * sizeof(float), device);
+    GemmArgs q = p;
+    q.batch = slices;
+    q.k = p.k / slices;
+    q.stride_a = p.trans_a ? q.k * p.lda : q.k;  // slice s starts at k = s q.k
+    q.stride_b = p.trans_b ? q.k : q.k * p.ldb;
+    q.alpha = 1.0f;
+    q.beta = 0.0f;
+    q.cin = nullptr;
+    q.c = ws.get();
+    q.ldc = p.n;
+    q.stride_c = mn;
+    launch_config<T, BM, BN, WM, WN, true>(q, stream);
+    const int64_t blocks = std::min<int64_t>((mn + kFinishBlock - 1) / kFinishBlock, 4 * int64_t{cu_count(device)});
+    splitk_finish16_kernel<T><<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
+        static_cast<const float*>(ws.get()), slices, p.m, p.n, p.alpha, p.beta, static_cast<const S*>(p.cin),
+        p.cin_rs, p.cin_cs, static_cast<S*>(p.c), p.ldc);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
@@ -1129,6 +1201,17 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
         const int64_t big_tiles = ((p.m + 255) / 256) * ((p.n + 255) / 256) * p.batch;
         if (big_tiles >= cu_count(device)) {
             launch_config<T, 256, 256, 2, 4>(p, stream);
+            return;
+        }
+        // Few 128 x 128 tiles and a long K (a Linear of a few hundred rows):
+        // split K, up to two blocks a CU, slices of at least 1024.  Measured
+        // (bf16, this split against the tiles alone): 128 x 11008 x 4096
+        // 36.4 against 57.7 us, 128 x 4096 x 4096 22.4 against 42.6 us,
+        // 1024 x 1024 x 8192 41.5 against 81.4 us; 1024^3 in slices of 512
+        // was slower (19.5 against 13.5 us) and is not split.
+        const int slices16 = splitk_slices(p, 2 * cu_count(device), 128, 1024, Mfma<T>::BK);
+        if (slices16 > 1) {
+            launch_splitk16<T, 128, 128, 2, 2>(p, slices16, stream, device);
             return;
         }
         // Too few 128 x 128 tiles for a quarter of the CUs (mm 1024^2 has

@@ -487,6 +487,49 @@ def test_gemm_fp32_split_k(amd, dev, orc, ta, tb, cin_kind):
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("cin_kind", ["none", "full", "bias-row"])
+def test_gemm16_split_k(amd, dev, orc, dtype, ta, tb, cin_kind):
+    """A 16-bit product with few 128 x 128 tiles and a long K (200 x 384
+    outputs, K = 4096: 6 tiles) is split over K into float32 partials, added
+    in slice order and rounded once: within the 16-bit bar of the float64
+    product with alpha = 0.5 and beta = 2 (a full Cin or a row-broadcast
+    bias), NaN-padded leading dimensions, a ragged M, and two runs giving
+    the same bits."""
+    lib = amd.load()
+    m, n, k, pad, alpha = 200, 384, 4096, 8, 0.5
+    a = _padded(orc, (k, m) if ta else (m, k), pad, dtype, 17)
+    b = _padded(orc, (n, k) if tb else (k, n), pad, dtype, 18)
+    A = orc.to_float(a, dtype).astype(np.float64)
+    B = orc.to_float(b, dtype).astype(np.float64)
+    A = A[:, :m].T if ta else A[:, :k]
+    B = B[:, :k].T if tb else B[:, :n]
+    want = alpha * (A @ B)
+    if cin_kind == "none":
+        beta, cin, rs, cs = 0.0, None, 0, 0
+    elif cin_kind == "full":
+        beta, cin, rs, cs = 2.0, sample(orc, (m, n), dtype, 19), n, 1
+        want = want + beta * orc.to_float(cin, dtype)
+    else:
+        beta, cin, rs, cs = 2.0, sample(orc, (n,), dtype, 19), 0, 1
+        want = want + beta * orc.to_float(cin, dtype)
+    da, db = dev.from_numpy(a, dtype=dtype), dev.from_numpy(b, dtype=dtype)
+    dc = dev.from_numpy(cin, dtype=dtype) if cin is not None else None
+    outs = []
+    for _ in range(2):
+        out = dev.empty((m, n), dtype=dtype)
+        st = lib.tp_amd_launch_gemm(0, dtype, 1, m, n, k, alpha, da.data_ptr, a.shape[-1], 0, int(ta),
+                                    db.data_ptr, b.shape[-1], 0, int(tb), beta,
+                                    dc.data_ptr if dc is not None else 0, rs, cs, 0, out.data_ptr, n, 0)
+        assert st == 0, lib.tp_mlu_last_error()
+        outs.append(out.numpy())
+    assert np.array_equal(outs[0], outs[1]), "split-K sum is not deterministic"
+    assert not np.isnan(orc.to_float(outs[0], dtype)).any(), "padding leaked into the product"
+    check(orc, outs[0], want, dtype, f"16-bit split-K ta={ta} tb={tb} {cin_kind}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
 @pytest.mark.parametrize("k", [64, 128])
 @pytest.mark.parametrize("cin_kind", ["none", "bias-row", "full"])
 @pytest.mark.parametrize("bt,m,n", [(64, 512, 512), (257, 256, 256)], ids=["xcd-order", "plain-order"])
