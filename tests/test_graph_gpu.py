@@ -203,3 +203,48 @@ def test_replay_nn_layers(dev, ops, orc, graph_mod, runtime):
     finally:
         g.reset()
     assert g.stats()[1] == 0
+
+
+def thin_step(ops, t):
+    """Products whose kernels fold partials across blocks: a thin product
+    with W K-major (tiles split over blocks, arrival counters), one with W
+    N-major and an odd K, and a 16-bit split-K product (float32 partials
+    and a finish kernel)."""
+    return (ops.linear(t["x"], t["w"]), ops.mm(t["dy"], t["w2"]), ops.mm(t["a"], t["b"]))
+
+
+def test_replay_thin_and_split_products(dev, ops, graph_mod, runtime):
+    """The recorded thin and split-K products replay to the eager bits on
+    every refilled input, with the same products run eagerly in between
+    (they share the arrival counters and the workspace pool)."""
+    rng = np.random.default_rng(9)
+    bf = lambda a: ops.to(dev.from_numpy(a.astype(np.float32)), 2)  # noqa: E731
+
+    def inputs():
+        return {"x": rng.standard_normal((1, 4096)), "dy": rng.standard_normal((1, 3001)),
+                "a": rng.standard_normal((200, 4096)) / 16}
+
+    fixed = {"w": bf(rng.standard_normal((2048, 4096)) / 64), "w2": bf(rng.standard_normal((3001, 1024)) / 64),
+             "b": bf(rng.standard_normal((4096, 384)) / 64)}
+    t = dict(fixed)
+    t.update({k: bf(v) for k, v in inputs().items()})
+    g = graph_mod.Graph()
+    try:
+        outs = g.capture(lambda: thin_step(ops, t))
+        for i in range(3):
+            host = {k: bf(v) for k, v in inputs().items()}
+            for k, v in host.items():
+                ops.copy_(t[k], v)                  # refill the recorded inputs
+            g.replay()
+            runtime.synchronize()
+            fresh = dict(fixed)
+            fresh.update(host)
+            want = thin_step(ops, fresh)            # eager, same kernels
+            for name, got, w in zip(("thin K-major", "thin N-major", "split-K"), outs, want):
+                assert_bitexact(got.numpy(), w.numpy(), f"replay {i}: {name} against eager")
+            del want, fresh
+            thin_step(ops, t)                       # eager products between replays
+            runtime.synchronize()
+    finally:
+        g.reset()
+    assert g.stats()[1] == 0
