@@ -199,3 +199,38 @@ def test_thin_after_repack(dev, ops, orc, dtype):
     got = ops.mm(dev.from_numpy(x, dtype=dtype), dev.from_numpy(w, dtype=dtype)).numpy()
     want = orc.to_float(x, dtype).astype(np.float64) @ orc.to_float(w, dtype).astype(np.float64)
     _check(orc, got, want, dtype, "thin product of a repacked operand")
+
+
+def test_thin_random_shapes(amd, dev, orc):
+    """Forty seeded random thin products: dtype, layout, thin side, row count
+    (1-64), K (with and without a partial last step; odd when W is N-major),
+    N ragged against the column tiles, batch (1-3, W shared or not), alpha,
+    beta and the Cin form all drawn at random; each against float64 at the
+    dtype's bar, and every one run twice for the same bits."""
+    lib = amd.load()
+    rng = np.random.default_rng(2024)
+    for case in range(40):
+        dtype = [F32, BF16, F16][rng.integers(3)]
+        v = 8 if dtype != F32 else 4
+        ta, tb = bool(rng.integers(2)), bool(rng.integers(2))
+        thin = int(rng.integers(1, 65))
+        wide = int(rng.integers(1, 40)) * 64 + int(rng.integers(0, 64))
+        k = int(rng.integers(2, 40)) * 64 + (int(rng.integers(0, 64)) // v) * v
+        if rng.integers(2):
+            m, n = thin, wide
+        else:
+            m, n = wide, thin
+        w_kmajor = tb if m <= n else not ta
+        if not w_kmajor:
+            k += int(rng.integers(1, v))  # a K that is not a whole number of packets
+        bt = int(rng.integers(1, 4))
+        alpha = float(rng.choice([1.0, 0.5, -2.0]))
+        kind = ["none", "bias-row", "full"][rng.integers(3)]
+        beta = 0.0 if kind == "none" else float(rng.choice([1.0, 2.0]))
+        shared = kind != "full" and bool(rng.integers(2))
+        what = (f"case {case}: {IDS[dtype]} {bt}x{m}x{n}x{k} ta={ta} tb={tb} alpha={alpha} "
+                f"{kind} beta={beta} shared={shared}")
+        outs, want = _run(lib, dev, orc, dtype, bt, m, n, k, ta, tb, alpha=alpha, beta=beta, cin_kind=kind,
+                          shared_b=shared, reps=2, seed=case)
+        assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8)), f"{what}: not deterministic"
+        _check(orc, outs[0], want, dtype, what)
