@@ -323,7 +323,7 @@ def thin_cases(ops, dev):
     for dtype in (BF16, F32):
         e = ESIZE[dtype]
         w = copies(put((11008, 4096), dtype, 4096 ** -0.5), 4)
-        for m in (1, 16):
+        for m in (1, 16, 64):
             x = put((m, 4096), dtype)
             cases.append((f"linear_{m}x4096x11008_{NAME[dtype]}", x, w, lambda x, w: ops.linear(x, w),
                           (11008 * 4096 + m * 4096 + m * 11008) * e))

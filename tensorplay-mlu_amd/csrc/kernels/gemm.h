@@ -22,6 +22,10 @@ struct GemmArgs {
     // C stored transposed: element (i, j) of the product at c + j ldc + i
     // (gemm_mfma_kernel only; set by the dispatch when it computes C^T).
     bool trans_c = false;
+    // Split-K partials of a 16-bit product (gemm_mfma_kernel's float32
+    // output): the product's whole K; batch entry s covers k = s k ..
+    // min((s + 1) k, k_total).
+    int64_t k_total = 0;
 };
 
 // Any shape, stride and alignment (gemm.hip).
@@ -31,6 +35,11 @@ void launch_gemm_general(const GemmArgs& p, hipStream_t stream);
 // Products with at most 64 rows or 64 columns whose large operand the
 // matrix cores can read in place (gemm_thin.hip); false when not eligible.
 bool launch_gemm_thin(int dtype, const GemmArgs& p, hipStream_t stream);
+
+// True when a 16-bit product of one matrix splits over K into at least one
+// 128 x 128-tile block a CU (gemm_mfma.hip).  The thin kernel leaves such
+// products of more than 32 rows to the split.
+bool splitk16_fills(const GemmArgs& p, int device);
 
 // Picks the matrix-core kernel when the operands allow it, the general one
 // otherwise (gemm_mfma.hip).

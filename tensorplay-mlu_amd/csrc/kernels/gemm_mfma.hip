@@ -284,13 +284,16 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int wm = wave / WN, wn = wave % WN;
     const int half = lane / 32, l32 = lane % 32;
-    const int64_t nk = (p.k + BK - 1) / BK;
 
     // One batch entry per blockIdx.z (the host launches batches of at most
     // 65535); a loop over the batch here would keep every address live
     // across it and spill.
     {
         const int64_t bi = blockIdx.z;
+        // Split-K partials: batch entry bi is the slice k = bi k .. of the
+        // product's k_total, the last one shorter when k does not divide it.
+        const int64_t kk = F32OUT && p.k_total - bi * p.k < p.k ? p.k_total - bi * p.k : p.k;
+        const int64_t nk = (kk + BK - 1) / BK;
         const S* A = static_cast<const S*>(p.a) + bi * p.stride_a;
         const S* B = static_cast<const S*>(p.b) + bi * p.stride_b;
         f32x16 acc[TM][TN];
@@ -304,13 +307,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
         LA la;
         LB lb;
         // Prologue: K tile 0 into stage 0, K tile 1 in flight.
-        la.load(A, p.lda, m0, p.m, 0, p.k);
-        lb.load(B, p.ldb, n0, p.n, 0, p.k);
+        la.load(A, p.lda, m0, p.m, 0, kk);
+        lb.load(B, p.ldb, n0, p.n, 0, kk);
         la.store(lds);
         lb.store(lds + BM * LDS_STRIDE);
         if (nk > 1) {
-            la.load(A, p.lda, m0, p.m, BK, p.k);
-            lb.load(B, p.ldb, n0, p.n, BK, p.k);
+            la.load(A, p.lda, m0, p.m, BK, kk);
+            lb.load(B, p.ldb, n0, p.n, BK, kk);
         }
         __syncthreads();
         for (int64_t kt = 0; kt < nk; ++kt) {
@@ -366,8 +369,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void gemm_mfma_kernel(GemmArgs p) 
                 lb.store(next + BM * LDS_STRIDE);
             }
             if (kt + 2 < nk) {
-                la.load(A, p.lda, m0, p.m, (kt + 2) * BK, p.k);
-                lb.load(B, p.ldb, n0, p.n, (kt + 2) * BK, p.k);
+                la.load(A, p.lda, m0, p.m, (kt + 2) * BK, kk);
+                lb.load(B, p.ldb, n0, p.n, (kt + 2) * BK, kk);
             }
             __syncthreads();
         }
@@ -1017,6 +1020,7 @@ void launch_config(const GemmArgs& whole, hipStream_t stream) {
         p.c = F32OUT ? static_cast<void*>(static_cast<float*>(whole.c) + b0 * whole.stride_c)
                      : static_cast<void*>(static_cast<S*>(whole.c) + b0 * whole.stride_c);
         if (whole.cin != nullptr) p.cin = static_cast<const S*>(whole.cin) + b0 * whole.cin_stride_b;
+        if (F32OUT) p.k_total = whole.k_total - b0 * whole.k;
         launch_chunk<T, BM, BN, WM, WN, F32OUT>(p, stream);
     }
 }
@@ -1112,14 +1116,39 @@ __global__ __launch_bounds__(kFinishBlock) void splitk_finish16_kernel(
     }
 }
 
+// The 16-bit split: the most slices that keep the 128 x 128 tiles times
+// the slices within max_blocks, with slices of a multiple of BK and at least
+// min_k; the last slice is shorter when K is not a multiple of the slice.
+struct SplitPlan {
+    int64_t slices = 1, ks = 0;
+};
+
+SplitPlan splitk16_plan(const GemmArgs& p, int64_t max_blocks, int64_t min_k, int64_t bk) {
+    SplitPlan plan;
+    if (p.batch != 1) return plan;
+    const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+    for (int64_t s = max_blocks / tiles; s > 1; --s) {
+        const int64_t ks = ((p.k + s - 1) / s + bk - 1) / bk * bk;
+        if (ks < min_k) continue;
+        plan.ks = ks;
+        plan.slices = (p.k + ks - 1) / ks;
+        break;
+    }
+    return plan;
+}
+
+constexpr int64_t kSplit16MinK = 1024;
+
 template <typename T, int BM, int BN, int WM, int WN>
-void launch_splitk16(const GemmArgs& p, int slices, hipStream_t stream, int device) {
+void launch_splitk16(const GemmArgs& p, const SplitPlan& plan, hipStream_t stream, int device) {
     using S = typename Elem<T>::storage;
     const int64_t mn = p.m * p.n;
+    const int64_t slices = plan.slices;
     Workspace ws(static_cast<size_t>(slices * mn) * sizeof(float), device);
     GemmArgs q = p;
     q.batch = slices;
-    q.k = p.k / slices;
+    q.k = plan.ks;
+    q.k_total = p.k;
     q.stride_a = p.trans_a ? q.k * p.lda : q.k;  // slice s starts at k = s q.k
     q.stride_b = p.trans_b ? q.k : q.k * p.ldb;
     q.alpha = 1.0f;
@@ -1131,7 +1160,7 @@ void launch_splitk16(const GemmArgs& p, int slices, hipStream_t stream, int devi
     launch_config<T, BM, BN, WM, WN, true>(q, stream);
     const int64_t blocks = std::min<int64_t>((mn + kFinishBlock - 1) / kFinishBlock, 4 * int64_t{cu_count(device)});
     splitk_finish16_kernel<T><<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
-        static_cast<const float*>(ws.get()), slices, p.m, p.n, p.alpha, p.beta, static_cast<const S*>(p.cin),
+        static_cast<const float*>(ws.get()), static_cast<int>(slices), p.m, p.n, p.alpha, p.beta, static_cast<const S*>(p.cin),
         p.cin_rs, p.cin_cs, static_cast<S*>(p.c), p.ldc);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
@@ -1209,9 +1238,9 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
         // 36.4 against 57.7 us, 128 x 4096 x 4096 22.4 against 42.6 us,
         // 1024 x 1024 x 8192 41.5 against 81.4 us; 1024^3 in slices of 512
         // was slower (19.5 against 13.5 us) and is not split.
-        const int slices16 = splitk_slices(p, 2 * cu_count(device), 128, 1024, Mfma<T>::BK);
-        if (slices16 > 1) {
-            launch_splitk16<T, 128, 128, 2, 2>(p, slices16, stream, device);
+        const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, Mfma<T>::BK);
+        if (plan.slices > 1) {
+            launch_splitk16<T, 128, 128, 2, 2>(p, plan, stream, device);
             return;
         }
         // Too few 128 x 128 tiles for a quarter of the CUs (mm 1024^2 has
@@ -1365,6 +1394,13 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool splitk16_fills(const GemmArgs& p, int device) {
+    const int cus = cu_count(device);
+    const SplitPlan plan = splitk16_plan(p, 2 * cus, kSplit16MinK, 64);
+    const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+    return plan.slices > 1 && tiles * plan.slices >= cus;
+}
 
 void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream) {
     if (launch_gemm_thin(dtype, p, stream)) return;

@@ -728,6 +728,16 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
     const bool xvec = q.x_k == 1 && q.k % V == 0 && aligned16(q.x) && (q.m == 1 || q.x_m % V == 0) &&
                       (p.batch == 1 || q.x_b % V == 0);
     if (q.m > thin_max_rows(sizeof(S) == 2, kmajor)) return false;
+    // Past 32 rows a 16-bit product that the split over K spreads over
+    // every CU runs faster there: bf16 33-64 x 11008 x 4096 (W K-major,
+    // rotated beyond the Infinity Cache) 31-34 us split against 41-44 us
+    // here.  Each wave here reads its 64 rows of X again for every 64
+    // columns of W.
+    if (sizeof(S) == 2 && q.m > 32) {
+        int device = 0;
+        TP_AMD_HIP_CHECK(hipGetDevice(&device));
+        if (splitk16_fills(p, device)) return false;
+    }
     if (kmajor) {
         launch_rows<T, true>(q, xvec, p.batch, stream);
     } else {

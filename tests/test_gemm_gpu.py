@@ -488,15 +488,18 @@ def test_gemm_fp32_split_k(amd, dev, orc, ta, tb, cin_kind):
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["NN", "TN", "NT", "TT"])
 @pytest.mark.parametrize("cin_kind", ["none", "full", "bias-row"])
-def test_gemm16_split_k(amd, dev, orc, dtype, ta, tb, cin_kind):
+@pytest.mark.parametrize("k", [4096, 4000, 3001])
+def test_gemm16_split_k(amd, dev, orc, dtype, ta, tb, cin_kind, k):
     """A 16-bit product with few 128 x 128 tiles and a long K (200 x 384
-    outputs, K = 4096: 6 tiles) is split over K into float32 partials, added
-    in slice order and rounded once: within the 16-bit bar of the float64
-    product with alpha = 0.5 and beta = 2 (a full Cin or a row-broadcast
-    bias), NaN-padded leading dimensions, a ragged M, and two runs giving
-    the same bits."""
+    outputs: 6 tiles) is split over K into float32 partials, added in slice
+    order and rounded once: within the 16-bit bar of the float64 product
+    with alpha = 0.5 and beta = 2 (a full Cin or a row-broadcast bias),
+    NaN-padded leading dimensions, a ragged M, and two runs giving the same
+    bits.  K = 4096 splits into four slices of 1024; K = 4000 into three of
+    1024 and a last of 928; K = 3001 (odd: K-major operands are copied with
+    zero padding first, M/N-major ones read in place) into 1536 and 1465."""
     lib = amd.load()
-    m, n, k, pad, alpha = 200, 384, 4096, 8, 0.5
+    m, n, pad, alpha = 200, 384, 8, 0.5
     a = _padded(orc, (k, m) if ta else (m, k), pad, dtype, 17)
     b = _padded(orc, (n, k) if tb else (k, n), pad, dtype, 18)
     A = orc.to_float(a, dtype).astype(np.float64)
@@ -524,7 +527,7 @@ def test_gemm16_split_k(amd, dev, orc, dtype, ta, tb, cin_kind):
         outs.append(out.numpy())
     assert np.array_equal(outs[0], outs[1]), "split-K sum is not deterministic"
     assert not np.isnan(orc.to_float(outs[0], dtype)).any(), "padding leaked into the product"
-    check(orc, outs[0], want, dtype, f"16-bit split-K ta={ta} tb={tb} {cin_kind}")
+    check(orc, outs[0], want, dtype, f"16-bit split-K k={k} ta={ta} tb={tb} {cin_kind}")
 
 
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])

@@ -108,6 +108,26 @@ def test_thin_up_to_128_rows(amd, dev, orc, dtype, ta, tb, m, n, k):
     _check(orc, got[0], want[0], dtype, f"thin {m}x{n}x{k} ta={ta} tb={tb}")
 
 
+# 33 to 64 thin rows of a 16-bit product whose split over K gives every CU
+# a block (at least 8193 wide columns with K = 4096: 65 tiles of 128, four
+# slices) leave the thin kernel for the split; K = 4100 has a last slice of
+# 836 after a copy of the K-major operands.
+SPLIT = [(40, 8200, 4096), (64, 8200, 4096), (48, 8200, 4100)]
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
+                         ids=["NN", "TN", "NT", "TT"])
+@pytest.mark.parametrize("m,n,k", SPLIT + [(n, m, k) for (m, n, k) in SPLIT],
+                         ids=[f"{m}x{n}x{k}" for (m, n, k) in SPLIT] + [f"{n}x{m}x{k}" for (m, n, k) in SPLIT])
+def test_thin_rows_past_32_split(amd, dev, orc, dtype, ta, tb, m, n, k):
+    lib = amd.load()
+    outs, want = _run(lib, dev, orc, dtype, 1, m, n, k, ta, tb, alpha=0.5, beta=2.0, cin_kind="bias-row",
+                      reps=2)
+    assert np.array_equal(outs[0], outs[1]), "two runs differ"
+    _check(orc, outs[0][0], want[0], dtype, f"split {m}x{n}x{k} ta={ta} tb={tb}")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: IDS[d])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)], ids=["NN", "NT", "TT"])
 @pytest.mark.parametrize("cin_kind", ["bias-row", "full"])
