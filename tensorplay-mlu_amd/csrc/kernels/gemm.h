@@ -36,10 +36,11 @@ void launch_gemm_general(const GemmArgs& p, hipStream_t stream);
 // matrix cores can read in place (gemm_thin.hip); false when not eligible.
 bool launch_gemm_thin(int dtype, const GemmArgs& p, hipStream_t stream);
 
-// True when a 16-bit product of one matrix splits over K into at least one
-// 128 x 128-tile block a CU (gemm_mfma.hip).  The thin kernel leaves such
-// products of more than 32 rows to the split.
-bool splitk16_fills(const GemmArgs& p, int device);
+// The blocks (128 x 128 tiles times K slices) that the 16-bit split over K
+// launches for a product of one matrix, 0 when it does not split, and the
+// slices (gemm_mfma.hip).  The thin kernel leaves products to the split
+// when these are enough to fill the CUs.
+int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices);
 
 // Picks the matrix-core kernel when the operands allow it, the general one
 // otherwise (gemm_mfma.hip).

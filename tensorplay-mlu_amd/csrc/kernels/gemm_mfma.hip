@@ -1395,11 +1395,11 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 
 }  // namespace
 
-bool splitk16_fills(const GemmArgs& p, int device) {
-    const int cus = cu_count(device);
-    const SplitPlan plan = splitk16_plan(p, 2 * cus, kSplit16MinK, 64);
+int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices) {
+    const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, 64);
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
-    return plan.slices > 1 && tiles * plan.slices >= cus;
+    *slices = plan.slices;
+    return plan.slices > 1 ? tiles * plan.slices : 0;
 }
 
 void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream) {

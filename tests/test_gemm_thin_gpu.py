@@ -108,11 +108,13 @@ def test_thin_up_to_128_rows(amd, dev, orc, dtype, ta, tb, m, n, k):
     _check(orc, got[0], want[0], dtype, f"thin {m}x{n}x{k} ta={ta} tb={tb}")
 
 
-# 33 to 64 thin rows of a 16-bit product whose split over K gives every CU
-# a block (at least 8193 wide columns with K = 4096: 65 tiles of 128, four
-# slices) leave the thin kernel for the split; K = 4100 has a last slice of
-# 836 after a copy of the K-major operands.
-SPLIT = [(40, 8200, 4096), (64, 8200, 4096), (48, 8200, 4100)]
+# 16-bit products of more than 16 thin rows leave the thin kernel for the
+# split over K when that gives the CUs enough blocks: past 32 rows one a CU
+# (8200 wide columns with K = 4096: 65 tiles of 128 times four slices), at
+# 17-32 rows a quarter more (10248 columns: 81 tiles, 324 blocks on 256
+# CUs).  K = 4100 has a last slice of 836 after a copy of the K-major
+# operands.
+SPLIT = [(40, 8200, 4096), (64, 8200, 4096), (48, 8200, 4100), (24, 10248, 4096)]
 
 
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=lambda d: IDS[d])
