@@ -306,10 +306,12 @@ def suite_gemm(ops, dev, ev):
     return out
 
 
-def thin_cases(ops, dev):
+def thin_cases(ops, dev, rows=(1, 16)):
     """Thin products of a decode step, each with its wide operand in several
     copies (rotated, so that the copies together exceed the 256 MB Infinity
-    Cache): (name, launch, bytes moved a launch, copies)."""
+    Cache): (name, launch, bytes moved a launch, copies).  ``rows``: the
+    Linear layer's batch rows (64 rows of a 16-bit product take the split
+    over K, not the thin kernel)."""
     g = np.random.default_rng(0)
 
     def put(shape, dtype, scale=1.0):
@@ -323,7 +325,7 @@ def thin_cases(ops, dev):
     for dtype in (BF16, F32):
         e = ESIZE[dtype]
         w = copies(put((11008, 4096), dtype, 4096 ** -0.5), 4)
-        for m in (1, 16, 64):
+        for m in rows:
             x = put((m, 4096), dtype)
             cases.append((f"linear_{m}x4096x11008_{NAME[dtype]}", x, w, lambda x, w: ops.linear(x, w),
                           (11008 * 4096 + m * 4096 + m * 11008) * e))
@@ -342,7 +344,7 @@ def suite_thin(ops, dev, ev):
     """Thin products (decode-step shapes): GB/s against HBM, the wide
     operand rotated over copies beyond the Infinity Cache."""
     out = {}
-    for name, x, ws, fn, nbytes in thin_cases(ops, dev):
+    for name, x, ws, fn, nbytes in thin_cases(ops, dev, rows=(1, 16, 64)):
         k = [0]
 
         def call(x=x, ws=ws, fn=fn):
