@@ -12,7 +12,9 @@
 // (element (k, j) at w + j ld + k: a Linear weight, or A of a product with
 // few columns) or N-major (at w + k ld + j: a [K, N] row-major matrix).
 // A product with few columns is taken as its transpose, C^T = B^T A^T, and
-// stores C' transposed (the output strides are free).
+// stores C' transposed (the output strides are free).  A 16-bit product of
+// more than 16 thin rows that gemm_mfma.hip's split over K spreads over
+// every CU is left to that split (see launch_typed).
 //
 // Work split.  A column tile of W (64 or 128 columns) over a step of K (64
 // of K for 16-bit types with W K-major) is one unit.  With at least as
