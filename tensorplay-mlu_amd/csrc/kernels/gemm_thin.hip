@@ -131,9 +131,12 @@ struct Thin {
     static constexpr int XL = KMAJOR ? HALVES : 1;                        // X fragments a row
     // Steps a batch of loads, and blocks a CU the registers are sized for
     // (float32 K-major with 17-32 rows: one packet a step at two blocks a
-    // CU, 32 x 11008 x 4096 in 47 us against 58 us at two and one block).
+    // CU, 32 x 11008 x 4096 in 47 us against 58 us at two and one block;
+    // 16-bit W N-major with up to 16 rows at two blocks a CU, the
+    // accumulators moved from AGPRs into the 256 VGPRs: the LM-head dX
+    // 1 x 50257 x 4096 80.5 against 84.8 us, other shapes level).
     static constexpr int U = KMAJOR ? (HALVES == 2 ? 8 : 4) / (NB * HALVES) : (k16 ? 1 : 8);
-    static constexpr int OCCUPANCY = (!k16 && KMAJOR && R == 2) ? 2 : 1;
+    static constexpr int OCCUPANCY = ((!k16 && KMAJOR && R == 2) || (k16 && !KMAJOR && R == 1)) ? 2 : 1;
     // X fragment: 8 (16-bit) or 4 (float32 K-major) consecutive k as one
     // packet, or one float.
     static constexpr bool kXPacket = k16 || KMAJOR;
