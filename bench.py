@@ -32,8 +32,8 @@ Also reported on the same line:
   section's unit, so every suite figure has a CPU figure beside it.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
-  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,vs_torch_thin,bmm,reduce,
-                             reduce_all,softmax,nn,mlp,odd,thin}   # launch sequences for rocprofv3
+  python bench.py --profile {traffic,traffic_cold,gemm,gemm32,linear,vs_torch,vs_torch_thin,vs_torch_batch,
+                             bmm,reduce,reduce_all,softmax,nn,mlp,odd,thin}   # launch sequences for rocprofv3
 """
 
 from __future__ import annotations
@@ -964,6 +964,9 @@ def profile_launches(what: str, lib, ops, dev) -> None:
              16 rows, x @ W with W [4096, 11008], an LM head's logits and
              dX), this library and torch interleaved as in vs_torch, each
              rotating over its own copies of the wide operand;
+    vs_torch_batch: bf16 products of a small batch (Linear of 32 and 64
+             rows, x @ W with 64 rows and W [4096, 11008]), this library and
+             torch interleaved as in vs_torch_thin;
     thin:    the thin products of the suite (decode-step Linear layers,
              an LM head's logits and dX), ten launches each, the wide
              operand rotated over its copies;
@@ -1070,10 +1073,10 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                     for _ in range(10):
                         fn()
                     drain()
-    elif what == "vs_torch_thin":
-        # Thin bf16 products of a decode step from this library and from
-        # torch on the same GPU, interleaved as in vs_torch, each library
-        # rotating over its own copies of the wide operand.
+    elif what in ("vs_torch_thin", "vs_torch_batch"):
+        # Thin bf16 products of a decode step (or of a small batch) from this
+        # library and from torch on the same GPU, interleaved as in vs_torch,
+        # each library rotating over its own copies of the wide operand.
         import torch
         F = torch.nn.functional
         g = np.random.default_rng(0)
@@ -1102,6 +1105,12 @@ def profile_launches(what: str, lib, ops, dev) -> None:
                  (lambda: ops.mm(x1[0], rot(wn)), lambda: torch.mm(tx1[0], rot(twn))),
                  (lambda: ops.linear(x1[0], rot(head)), lambda: F.linear(tx1[0], rot(thead))),
                  (lambda: ops.mm(dy[0], rot(head)), lambda: torch.mm(tdy[0], rot(thead)))]
+        if what == "vs_torch_batch":
+            x32, tx32 = both((32, 4096))
+            x64, tx64 = both((64, 4096))
+            cases = [(lambda: ops.linear(x32[0], rot(w)), lambda: F.linear(tx32[0], rot(tw))),
+                     (lambda: ops.linear(x64[0], rot(w)), lambda: F.linear(tx64[0], rot(tw))),
+                     (lambda: ops.mm(x64[0], rot(wn)), lambda: torch.mm(tx64[0], rot(twn)))]
 
         def drain():
             assert lib.tp_amd_synchronize(0) == 0
@@ -1218,7 +1227,7 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--profile", choices=["traffic", "traffic_cold", "gemm", "gemm32", "linear", "vs_torch", "bmm",
                                          "reduce", "reduce_all", "softmax", "nn", "mlp", "odd", "thin",
-                                         "vs_torch_thin"],
+                                         "vs_torch_thin", "vs_torch_batch"],
                    help="run a fixed launch sequence for rocprofv3 and exit")
     args = p.parse_args()
     if args.gpus != 1:
@@ -1226,7 +1235,7 @@ def main() -> int:
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         return 2
 
-    if args.profile in ("vs_torch", "vs_torch_thin"):
+    if args.profile in ("vs_torch", "vs_torch_thin", "vs_torch_batch"):
         # torch's GPU path loads its own copy of the HIP runtime by a name
         # this library does not ask for; loaded first, it is the one copy in
         # the process, and this library binds to it by soname.  Loaded after
