@@ -1171,8 +1171,8 @@ void launch_splitk16(const GemmArgs& p, const SplitPlan& plan, hipStream_t strea
     launch_config<T, BM, BN, WM, WN, true>(q, stream);
     const int64_t blocks = std::min<int64_t>((mn + kFinishBlock - 1) / kFinishBlock, 4 * int64_t{cu_count(device)});
     splitk_finish16_kernel<T><<<static_cast<unsigned>(blocks), kFinishBlock, 0, stream>>>(
-        static_cast<const float*>(ws.get()), static_cast<int>(slices), p.m, p.n, p.alpha, p.beta, static_cast<const S*>(p.cin),
-        p.cin_rs, p.cin_cs, static_cast<S*>(p.c), p.ldc);
+        static_cast<const float*>(ws.get()), static_cast<int>(slices), p.m, p.n, p.alpha, p.beta,
+        static_cast<const S*>(p.cin), p.cin_rs, p.cin_cs, static_cast<S*>(p.c), p.ldc);
     TP_AMD_HIP_CHECK(hipGetLastError());
 }
 
@@ -1407,7 +1407,7 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 }  // namespace
 
 int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices) {
-    const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, 64);
+    const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, Mfma<bf16_t>::BK);
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
     *slices = plan.slices;
     return plan.slices > 1 ? tiles * plan.slices : 0;
