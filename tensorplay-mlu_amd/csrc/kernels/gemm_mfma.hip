@@ -1128,13 +1128,23 @@ __global__ __launch_bounds__(kFinishBlock) void splitk_finish16_kernel(
 }
 
 // The 16-bit split: the most slices that keep the 128 x 128 tiles times
-// the slices within max_blocks, with slices of a multiple of BK and at least
-// min_k; the last slice is shorter when K is not a multiple of the slice.
+// the slices within two blocks a CU, with slices of a multiple of BK and at
+// least kSplit16MinK; the last slice is shorter when K is not a multiple of
+// the slice.  A product of one row of tiles (a small batch, min(M, N) <=
+// 128) takes slices of kSplit16ShortK when that still gives every CU a
+// block: bf16 17-64 x 11008 x 4096 26-32 us against 29-34 us, 128 x 4096
+// x 4096 22.4 against 24.5 us (W rotated beyond the Infinity Cache).  With
+// more rows of tiles the extra partials cost more than the blocks gain
+// (256 x 4096 x 4096 30.9 against 29.1 us), and 1024^3 in slices of 512
+// ran 19.5 against 13.5 us unsplit.
 struct SplitPlan {
     int64_t slices = 1, ks = 0;
 };
 
-SplitPlan splitk16_plan(const GemmArgs& p, int64_t max_blocks, int64_t min_k, int64_t bk) {
+constexpr int64_t kSplit16MinK = 1024;
+constexpr int64_t kSplit16ShortK = 512;
+
+SplitPlan splitk16_slices(const GemmArgs& p, int64_t max_blocks, int64_t min_k, int64_t bk) {
     SplitPlan plan;
     if (p.batch != 1) return plan;
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
@@ -1148,7 +1158,14 @@ SplitPlan splitk16_plan(const GemmArgs& p, int64_t max_blocks, int64_t min_k, in
     return plan;
 }
 
-constexpr int64_t kSplit16MinK = 1024;
+SplitPlan splitk16_plan(const GemmArgs& p, int64_t cus, int64_t bk) {
+    if (std::min(p.m, p.n) <= 128) {
+        const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
+        const SplitPlan short_plan = splitk16_slices(p, 2 * cus, kSplit16ShortK, bk);
+        if (short_plan.slices > 1 && tiles * short_plan.slices >= cus) return short_plan;
+    }
+    return splitk16_slices(p, 2 * cus, kSplit16MinK, bk);
+}
 
 template <typename T, int BM, int BN, int WM, int WN>
 void launch_splitk16(const GemmArgs& p, const SplitPlan& plan, hipStream_t stream, int device) {
@@ -1244,12 +1261,12 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
             return;
         }
         // Few 128 x 128 tiles and a long K (a Linear of a few hundred rows):
-        // split K, up to two blocks a CU, slices of at least 1024.  Measured
+        // split K (splitk16_plan), up to two blocks a CU.  Measured
         // (bf16, this split against the tiles alone): 128 x 11008 x 4096
         // 36.4 against 57.7 us, 128 x 4096 x 4096 22.4 against 42.6 us,
         // 1024 x 1024 x 8192 41.5 against 81.4 us; 1024^3 in slices of 512
         // was slower (19.5 against 13.5 us) and is not split.
-        const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, Mfma<T>::BK);
+        const SplitPlan plan = splitk16_plan(p, cu_count(device), Mfma<T>::BK);
         if (plan.slices > 1) {
             launch_splitk16<T, 128, 128, 2, 2>(p, plan, stream, device);
             return;
@@ -1407,7 +1424,7 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 }  // namespace
 
 int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices) {
-    const SplitPlan plan = splitk16_plan(p, 2 * cu_count(device), kSplit16MinK, Mfma<bf16_t>::BK);
+    const SplitPlan plan = splitk16_plan(p, cu_count(device), Mfma<bf16_t>::BK);
     const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128);
     *slices = plan.slices;
     return plan.slices > 1 ? tiles * plan.slices : 0;

@@ -734,21 +734,22 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
                       (p.batch == 1 || q.x_b % V == 0);
     if (q.m > thin_max_rows(sizeof(S) == 2, kmajor)) return false;
     // A 16-bit product of more than 16 rows that the split over K spreads
-    // over every CU runs faster there, from 17 rows only when it takes at
-    // most four slices.  Each wave here reads its rows of X again for every
-    // 64 columns of W, which costs more as the rows grow, and a long K
-    // splits into many slices, each adding a float32 partial of C.
-    // Measured (bf16, W rotated beyond the Infinity Cache, x W^T / x W, us):
-    //   33-64 x 11008 x 4096 (86 tiles x 4 slices):  split 31-34 / 35-39, here 41-44 / -
-    //   33-64 x 4096 x 11008 (32 tiles x 10 slices): split 33-35 / 37-40, here 34-38 / -
-    //   17-32 x 11008 x 4096 (86 x 4):  split 29-31 / 32-35, here 31-34 / 37-40
-    //   17-32 x 4096 x 11008 (32 x 10): split 31-33 / 36-37, here 27-30 / 34-35
+    // over every CU runs faster there; from 17 to 32 rows with W K-major
+    // only when it takes at most eight slices.  Each wave here reads its
+    // rows of X again for every 64 columns of W, which costs more as the
+    // rows grow, and a long K splits into many slices, each adding a
+    // float32 partial of C.  Measured (bf16, W rotated beyond the Infinity
+    // Cache, x W^T / x W, us):
+    //   33-64 x 11008 x 4096 (86 tiles x 5 slices):  split 31-32 / 35-36, here 41-44 / -
+    //   33-64 x 4096 x 11008 (32 tiles x 16 slices): split 31-32 / 33-35, here 34-38 / -
+    //   17-32 x 11008 x 4096 (86 x 5):  split 26-29 / 30-32, here 29-31 / 33-35
+    //   17-32 x 4096 x 11008 (32 x 16): split 28-29 / 31-32, here 27-30 / 34-35
     if (sizeof(S) == 2 && q.m > 16) {
         int device = 0;
         TP_AMD_HIP_CHECK(hipGetDevice(&device));
         int64_t slices = 1;
         const int64_t blocks = splitk16_blocks(p, device, &slices);
-        if (blocks >= cu_count(device) && (q.m > 32 || slices <= 4)) return false;
+        if (blocks >= cu_count(device) && (q.m > 32 || !kmajor || slices <= 8)) return false;
     }
     if (kmajor) {
         launch_rows<T, true>(q, xvec, p.batch, stream);
