@@ -291,14 +291,16 @@ def _padded(orc, shape, pad, dtype, seed):
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["NN", "TN", "NT", "TT"])
-@pytest.mark.parametrize("bt,m,n,k", [(256, 256, 256, 256), (64, 512, 512, 320)],
-                         ids=["big-tiles", "K-tail-fallback"])
+@pytest.mark.parametrize("bt,m,n,k", [(256, 256, 256, 256), (256, 256, 256, 384), (64, 512, 512, 320)],
+                         ids=["big-tiles", "big-tiles-6-steps", "K-tail-fallback"])
 def test_gemm_abi_padded_batched(amd, dev, orc, dtype, ta, tb, bt, m, n, k):
     """tp_amd_launch_gemm on a batch of products with padded leading
     dimensions (NaN padding), alpha = 0.5 and beta = 2 with a full Cin.  The
-    first shape has one 256 x 256 tile per CU and four K tiles (the
-    four-wave kernel); the second, K = 320, is not a multiple of 128 and
-    takes the eight-wave kernel."""
+    first two shapes have one 256 x 256 tile per CU and four or six K tiles
+    (the four-wave kernel: its loads of A for the K tile after next go out
+    after each step's barrier, so the step pairs, the last two steps and
+    the prologue all issue differently); the third, K = 320, is not a
+    multiple of 128 and takes the eight-wave kernel."""
     lib = amd.load()
     pad, alpha, beta = 8, 0.5, 2.0
     a = _padded(orc, (bt, k, m) if ta else (bt, m, k), pad, dtype, 1)
