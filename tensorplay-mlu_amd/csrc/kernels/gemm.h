@@ -42,6 +42,10 @@ bool launch_gemm_thin(int dtype, const GemmArgs& p, hipStream_t stream);
 // when these are enough to fill the CUs.
 int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices);
 
+// True when a float32 product of 33-64 thin rows against a wide operand
+// goes to gemm_mfma.hip's split over K on 64 x 64 tiles.
+bool splitk32_takes(const GemmArgs& p, int device);
+
 // Picks the matrix-core kernel when the operands allow it, the general one
 // otherwise (gemm_mfma.hip).
 void launch_gemm(int dtype, const GemmArgs& p, hipStream_t stream);

@@ -1071,6 +1071,19 @@ __device__ __forceinline__ float sum_slices(const float* part, int slices, int64
     return acc;
 }
 
+// A float32 product of 33 to 64 rows (or columns) against a wide operand of
+// at least 128 tiles of 64 (a small batch through a Linear of 8192 or more
+// outputs): 64 x 64 tiles of two waves, K split up to four blocks a CU.
+// The thin kernel leaves these here.  Measured (64 x 11008 x 4096, W
+// rotated beyond the Infinity Cache): x W^T 91-95 against 104-114 us on
+// the thin kernel, x W 94-102 against 106-140 us; with 4096 columns (64
+// tiles) the thin kernel stays faster (101-110 against 109-114 us).
+int splitk32_small_batch(const GemmArgs& p, int cus) {
+    const int64_t thin = std::min(p.m, p.n), wide = std::max(p.m, p.n);
+    if (p.batch != 1 || thin <= 32 || thin > 64 || (wide + 63) / 64 < 128) return 1;
+    return splitk_slices(p, 4 * cus, 64);
+}
+
 // c = alpha * sum of the slices (+ beta Cin), the same expressions as the
 // kernels' epilogue; one thread an element, consecutive threads along a row.
 __global__ __launch_bounds__(kFinishBlock) void splitk_finish_kernel(const float* part, int slices, int64_t m,
@@ -1217,6 +1230,11 @@ void launch_mfma(const GemmArgs& p, hipStream_t stream) {
     TP_AMD_HIP_CHECK(hipGetDevice(&device));
     if constexpr (std::is_same<T, float>::value) {
         const int cus = cu_count(device);
+        const int batch_split = splitk32_small_batch(p, cus);
+        if (batch_split > 1) {
+            launch_splitk<64, 64, 2, 1>(p, batch_split, stream, device);
+            return;
+        }
         const int64_t tiles = ((p.m + 127) / 128) * ((p.n + 127) / 128) * p.batch;
         const int slices = splitk_slices(p, cus);
         // A [M, K] K-contiguous with B [K, N] N-contiguous (plain mm, and
@@ -1437,6 +1455,8 @@ void launch_typed(const GemmArgs& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool splitk32_takes(const GemmArgs& p, int device) { return splitk32_small_batch(p, cu_count(device)) > 1; }
 
 int64_t splitk16_blocks(const GemmArgs& p, int device, int64_t* slices) {
     const SplitPlan plan = splitk16_plan(p, cu_count(device), Mfma<bf16_t>::BK);

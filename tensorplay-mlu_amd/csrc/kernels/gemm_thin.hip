@@ -751,6 +751,11 @@ bool launch_typed(const GemmArgs& p, hipStream_t stream) {
         const int64_t blocks = splitk16_blocks(p, device, &slices);
         if (blocks >= cu_count(device) && (q.m > 32 || !kmajor || slices <= 8)) return false;
     }
+    if (sizeof(S) == 4 && q.m > 32) {
+        int device = 0;
+        TP_AMD_HIP_CHECK(hipGetDevice(&device));
+        if (splitk32_takes(p, device)) return false;
+    }
     if (kmajor) {
         launch_rows<T, true>(q, xvec, p.batch, stream);
     } else {

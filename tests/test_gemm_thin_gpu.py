@@ -109,15 +109,16 @@ def test_thin_up_to_128_rows(amd, dev, orc, dtype, ta, tb, m, n, k):
 
 
 # 16-bit products of more than 16 thin rows leave the thin kernel for the
-# split over K when that gives the CUs enough blocks: past 32 rows one a CU
-# (8200 wide columns with K = 4096: 65 tiles of 128 times four slices), at
-# 17-32 rows a quarter more (10248 columns: 81 tiles, 324 blocks on 256
-# CUs).  K = 4100 has a last slice of 836 after a copy of the K-major
-# operands.
+# split over K when that gives every CU a block (8200 wide columns with K =
+# 4096: 65 tiles of 128 times seven slices of 640, the last 256; 10248
+# columns and 24 rows: 81 tiles times six slices).  K = 4100 has a last
+# slice of 260 after a copy of the K-major operands.  float32 products of
+# 33-64 rows against at least 128 tiles of 64 columns take the split on
+# 64 x 64 tiles (8200 columns; K = 4100 does not split and stays thin).
 SPLIT = [(40, 8200, 4096), (64, 8200, 4096), (48, 8200, 4100), (24, 10248, 4096)]
 
 
-@pytest.mark.parametrize("dtype", [BF16, F16], ids=lambda d: IDS[d])
+@pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=lambda d: IDS[d])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)],
                          ids=["NN", "TN", "NT", "TT"])
 @pytest.mark.parametrize("m,n,k", SPLIT + [(n, m, k) for (m, n, k) in SPLIT],
